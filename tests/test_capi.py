@@ -1,0 +1,86 @@
+"""CPU checks of the C-ABI boundary: the library loads, exports every entry
+point include/helios_attn.h declares, and its host-only paths (argument
+checks, workspace sizing) behave.  No kernel is launched."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch  # noqa: F401  (loads torch's HIP runtime before the library)
+
+from helios_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "helios_attn.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[\w\s\*]*?\b(hpa_\w+)\s*\(", text, re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _lib.LIB_PATH.exists():
+        pytest.fail("libheliosattn.so is not built; run python -m helios_amd.build")
+    return _lib.load_library()
+
+
+def test_header_declares_the_expected_entry_points():
+    assert _declared() == sorted([
+        "hpa_version", "hpa_last_error", "hpa_decode_workspace_size", "hpa_paged_decode",
+        "hpa_paged_prefill", "hpa_kv_write", "hpa_kv_gather", "hpa_copy_blocks",
+    ])
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in _declared():
+        assert hasattr(lib, name), f"{name} declared in helios_attn.h but not exported"
+    assert set(_declared()) == set(_lib.SIGNATURES)
+
+
+def test_version_matches_header(lib):
+    m = re.search(r"#define HPA_VERSION (\d+)", HEADER.read_text())
+    assert lib.hpa_version() == int(m.group(1))
+
+
+def test_status_codes_match_header():
+    text = HEADER.read_text()
+    for name in ("HPA_OK", "HPA_ERR_ARG", "HPA_ERR_UNSUPPORTED", "HPA_ERR_WORKSPACE",
+                 "HPA_ERR_LAUNCH", "HPA_F32", "HPA_F16", "HPA_BF16", "HPA_I8"):
+        m = re.search(rf"#define {name} (\d+)", text)
+        assert int(m.group(1)) == getattr(_lib, name), name
+
+
+def test_workspace_size(lib):
+    # one partition per sequence -> no workspace
+    assert lib.hpa_decode_workspace_size(64, 1, 14, 2, 64, 256, 256) == 0
+    # split: seqs * Hkv * parts * rows * (D + 2) floats
+    got = lib.hpa_decode_workspace_size(4, 3, 32, 8, 128, 2048, 512)
+    assert got == 4 * 8 * 4 * 12 * 130 * 4
+
+
+def test_argument_errors_return_status_without_a_gpu(lib):
+    st = lib.hpa_paged_decode(None, None, 0, None, None, 0, None, None, 0, None, 1, None, 1, 1,
+                              1, 1, 64, 16, 1, 16, 1.0, 0, None, 0, None)
+    assert st == _lib.HPA_ERR_ARG
+    assert b"null pointer" in lib.hpa_last_error()
+    dummy = ctypes.c_void_p(16)
+    st = lib.hpa_paged_decode(dummy, dummy, 1, dummy, dummy, 1, None, None, 0, dummy, 1, dummy,
+                              1, 1, 4, 2, 64, 12, 8, 16, 1.0, 0, None, 0, None)
+    assert st == _lib.HPA_ERR_UNSUPPORTED and b"block_size 12" in lib.hpa_last_error()
+    st = lib.hpa_paged_decode(dummy, dummy, 1, dummy, dummy, 1, None, None, 0, dummy, 1, dummy,
+                              1, 1, 4, 2, 48, 16, 8, 16, 1.0, 0, None, 0, None)
+    assert st == _lib.HPA_ERR_UNSUPPORTED and b"head_dim 48" in lib.hpa_last_error()
+    st = lib.hpa_paged_decode(dummy, dummy, 1, dummy, dummy, 1, None, None, 0, dummy, 1, dummy,
+                              1, 9, 8, 1, 64, 16, 8, 16, 1.0, 0, None, 0, None)
+    assert st == _lib.HPA_ERR_UNSUPPORTED and b"exceed 64" in lib.hpa_last_error()
+    # int8 without scales
+    st = lib.hpa_kv_write(dummy, dummy, 1, dummy, dummy, 3, None, None, 1, dummy, 1, dummy, dummy,
+                          1, 1, 2, 64, 16, 8, None)
+    assert st == _lib.HPA_ERR_ARG
+    # empty batches are no-ops
+    assert lib.hpa_paged_prefill(None, None, 0, None, None, 0, None, None, 0, None, 1, None, None,
+                                 None, 0, 0, 1, 1, 64, 16, 1, 1.0, None) == _lib.HPA_OK

@@ -1,0 +1,145 @@
+"""GPU parity of the KV-cache kernels: quantize+scatter write (bit-exact int8
+payload and scales), fp scatter, gather/dequant and batched block copies."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helios_amd import PagedKVCache, QuantizedPagedKVCache, copy_blocks, write_kv
+from oracle import paged_ref as R
+from tests.gpu_util import to_np
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("in_dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("scale_dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("D", [16, 64, 128, 256])
+def test_int8_write_is_bit_exact(in_dtype, scale_dtype, D):
+    gen = torch.Generator().manual_seed(D)
+    bs, H, nb = 16, 2, 20
+    cache = QuantizedPagedKVCache(nb, bs, H, D, dtype=torch.float16, device="cuda",
+                                  scale_dtype=scale_dtype)
+    pool = R.PagedPool(nb, bs, H, D, np.float32, quantized=True,
+                       scale_dtype=np.float16 if scale_dtype == torch.float16 else np.float32)
+    blocks = [7, 3, 19, 0]
+    # mixed magnitudes, exact zeros rows and .5 ties after scaling
+    k = (torch.randn(50, H, D, generator=gen) * torch.rand(50, H, 1, generator=gen) * 10)
+    v = torch.randn(50, H, D, generator=gen)
+    k[3] = 0.0
+    v[4, 0, :] = torch.arange(D, dtype=torch.float32) - D / 2
+    k, v = k.to(in_dtype), v.to(in_dtype)
+    cache.write(blocks, 5, k.cuda(), v.cuda())
+    pool.write(blocks, 5, k.float().numpy(), v.float().numpy())
+    assert np.array_equal(to_np(cache.k_cache), pool.k)
+    assert np.array_equal(to_np(cache.v_cache), pool.v)
+    assert np.array_equal(to_np(cache.k_scale).view(np.uint8), pool.k_scale.view(np.uint8))
+    assert np.array_equal(to_np(cache.v_scale).view(np.uint8), pool.v_scale.view(np.uint8))
+
+
+def test_config3_new_token_write_per_sequence():
+    """Config 3's write: one new token per sequence for 64 sequences, at
+    position ctx - 1 through each sequence's table, fp16 input."""
+    rng = np.random.default_rng(3)
+    gen = torch.Generator().manual_seed(3)
+    B, H, D, bs = 64, 2, 64, 16
+    lens = rng.integers(512, 4097, size=B)
+    need = [(int(c) + bs - 1) // bs for c in lens]
+    nb = sum(need)
+    ids = rng.permutation(nb)
+    tables, o = [], 0
+    for n in need:
+        tables.append([int(x) for x in ids[o:o + n]])
+        o += n
+    cache = QuantizedPagedKVCache(nb, bs, H, D, dtype=torch.float16, device="cuda")
+    pool = R.PagedPool(nb, bs, H, D, np.float32, quantized=True)
+    k = torch.randn(B, H, D, generator=gen).half()
+    v = torch.randn(B, H, D, generator=gen).half()
+    starts = [int(c) - 1 for c in lens]
+    write_kv(cache, tables, starts, k.cuda(), v.cuda(), query_lens=[1] * B)
+    for b in range(B):
+        pool.write(tables[b], starts[b], k[b:b + 1].float().numpy(), v[b:b + 1].float().numpy())
+    assert np.array_equal(to_np(cache.k_cache), pool.k)
+    assert np.array_equal(to_np(cache.v_cache), pool.v)
+    assert np.array_equal(to_np(cache.k_scale), pool.k_scale)
+    assert np.array_equal(to_np(cache.v_scale), pool.v_scale)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_fp_write_and_gather_round_trip(dtype):
+    """reference tests/parity/test_parity.py:134-142 on the device."""
+    cache = PagedKVCache(16, 4, 2, 8, dtype=dtype, device="cuda")
+    blocks = [11, 2, 7]
+    k = torch.randn(10, 2, 8, device="cuda").to(dtype)
+    v = torch.randn(10, 2, 8, device="cuda").to(dtype)
+    cache.write(blocks, 0, k, v)
+    gk, gv = cache.gather(blocks, 10)
+    assert torch.equal(gk, k) and torch.equal(gv, v)
+    # input dtype differing from the pool's is rounded to the pool's
+    k32 = torch.randn(3, 2, 8, device="cuda")
+    cache.write(blocks, 4, k32, k32)
+    gk, _ = cache.gather(blocks, 7)
+    assert torch.equal(gk[4:7], k32.to(dtype))
+
+
+def test_int8_gather_dequantises_like_helios():
+    gen = torch.Generator().manual_seed(0)
+    cache = QuantizedPagedKVCache(8, 16, 2, 64, dtype=torch.float16, device="cuda")
+    pool = R.PagedPool(8, 16, 2, 64, np.float16, quantized=True)
+    k = torch.randn(30, 2, 64, generator=gen)
+    cache.write([5, 1], 0, k.cuda(), k.cuda())
+    pool.write([5, 1], 0, k.numpy(), k.numpy())
+    gk, gv = cache.gather([5, 1], 30)
+    wk, wv = pool.gather([5, 1], 30)
+    assert np.array_equal(to_np(gk), wk) and np.array_equal(to_np(gv), wv)
+
+
+def test_partial_block_write_and_out_of_range():
+    """reference tests/quant/test_kv_quant.py:134-152."""
+    cache = QuantizedPagedKVCache(8, 16, 2, 64, dtype=torch.float16, device="cuda")
+    first = torch.randn(4, 2, 64, device="cuda")
+    cache.write([0], 0, first, first)
+    snap, _ = cache.gather([0], 4)
+    cache.write([0], 4, first * 50, first * 50)
+    again, _ = cache.gather([0], 4)
+    assert torch.equal(snap, again)
+    k = torch.randn(20, 2, 64, device="cuda")
+    with pytest.raises(IndexError, match="position 16 needs logical block 1"):
+        cache.write([1], 0, k, k)
+    # helios writes the positions before the failing one
+    got, _ = cache.gather([1], 16)
+    ref = QuantizedPagedKVCache(8, 16, 2, 64, dtype=torch.float16, device="cuda")
+    ref.write([1], 0, k[:16], k[:16])
+    want, _ = ref.gather([1], 16)
+    assert torch.equal(got, want)
+
+
+def test_copy_block_moves_scales():
+    """reference tests/quant/test_kv_quant.py:112-131."""
+    cache = QuantizedPagedKVCache(8, 16, 2, 64, dtype=torch.float16, device="cuda")
+    large = torch.randn(16, 2, 64, device="cuda") * 1000
+    small = torch.randn(16, 2, 64, device="cuda") * 0.001
+    cache.write([0], 0, large, large)
+    cache.write([1], 0, small, small)
+    cache.copy_block(0, 1)
+    a, _ = cache.gather([0], 16)
+    b, _ = cache.gather([1], 16)
+    assert torch.equal(a, b) and b.abs().max().item() > 100
+
+
+def test_copy_blocks_all_layers_one_launch():
+    caches = [PagedKVCache(10, 16, 2, 32, dtype=torch.float16, device="cuda") for _ in range(3)]
+    for c in caches:
+        c.k_cache.normal_()
+        c.v_cache.normal_()
+    before = [(c.k_cache.clone(), c.v_cache.clone()) for c in caches]
+    pairs = [(1, 4), (2, 5), (4, 9)]  # (4, 9) reads a block written earlier in the list
+    copy_blocks(caches, pairs)
+    for (k0, v0), c in zip(before, caches):
+        kk, vv = k0.clone(), v0.clone()
+        for s, d in pairs:  # sequential semantics
+            kk[d] = kk[s]
+            vv[d] = vv[s]
+        assert torch.equal(c.k_cache, kk) and torch.equal(c.v_cache, vv)

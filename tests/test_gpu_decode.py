@@ -1,0 +1,229 @@
+"""GPU parity of the paged decode / verify kernel (hpa_paged_decode) against
+the oracle, on seeded inputs.
+
+Tolerances (stated by the build's target): fp16 output max-abs <= 2e-3 against
+a float64 reference computed from the same rounded inputs (int8 values
+dequantised with the stored scales); bf16 gets one bf16 half-ulp of the
+reference on top (output rounding alone nearly fills 2e-3 there); fp32 KV
+(the toy-model path) <= 2e-5.  Batch-order invariance is asserted bit-exact.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from helios_amd import (
+    PagedKVCache,
+    QuantizedPagedKVCache,
+    paged_attention_decode,
+    paged_attention_decode_batched,
+    paged_attention_decode_hip,
+    paged_attention_verify_batched,
+)
+from oracle import paged_ref as R
+from tests.gpu_util import dev, fill_cache, max_abs, pool_of, ragged_tables, to_np
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float16: 2e-3, torch.bfloat16: 2e-3, torch.float32: 2e-5}
+
+
+def _tol(dtype, want):
+    t = TOL[dtype]
+    if dtype == torch.bfloat16:
+        return t + np.abs(want) * 2.0 ** -9
+    return t
+
+
+def _check(got: torch.Tensor, want: np.ndarray, dtype, what=""):
+    g = to_np(got).astype(np.float64)
+    assert np.isfinite(g).all(), f"{what}: non-finite output"
+    err = np.abs(g - want)
+    bound = _tol(dtype, want)
+    assert (err <= bound).all(), f"{what}: max-abs {err.max():.3e}"
+
+
+def _case(seed, n_seqs, lens, Hq, Hkv, D, bs, dtype, quant=False, scale_dtype=torch.float16,
+          q_per_seq=1, extra_blocks=3):
+    gen = torch.Generator().manual_seed(seed)
+    rng = np.random.default_rng(seed)
+    nb = sum((c + bs - 1) // bs for c in lens) + extra_blocks
+    if quant:
+        cache = QuantizedPagedKVCache(nb, bs, Hkv, D, dtype=dtype, device="cuda",
+                                      scale_dtype=scale_dtype)
+    else:
+        cache = PagedKVCache(nb, bs, Hkv, D, dtype=dtype, device="cuda")
+    fill_cache(cache, gen)
+    tables = ragged_tables(rng, lens, bs, nb)
+    q = torch.randn(n_seqs * q_per_seq, Hq, D, generator=gen).to(dtype).to(dev())
+    return cache, tables, q
+
+
+def _oracle_decode(cache, q, tables, lens, scale=None, q_per_seq=1):
+    pool = pool_of(cache)
+    qn = to_np(q).astype(np.float32)
+    if q_per_seq == 1:
+        return R.paged_decode_batched(qn, pool, tables, lens, scale)
+    return R.paged_verify_batched(qn, pool, tables, lens, q_per_seq, scale)
+
+
+@pytest.mark.parametrize("n_seqs", [1, 4, 17])
+@pytest.mark.parametrize("block_size", [16, 32])
+def test_decode_matches_oracle_reference_shapes(n_seqs, block_size):
+    """Shapes of reference tests/parity/test_triton_parity.py:50-86: ragged
+    contexts bs*(i%3+1) - (i%bs), Hq 8 / Hkv 2 / D 64, fp16, tables strided
+    by 7 through a 256-block pool."""
+    torch.manual_seed(0)
+    n_kv, n_q, D, n_blocks = 2, 8, 64, 256
+    cache = PagedKVCache(n_blocks, block_size, n_kv, D, dtype=torch.float16, device="cuda")
+    cache.k_cache.normal_()
+    cache.v_cache.normal_()
+    lens, tables, used = [], [], 0
+    for i in range(n_seqs):
+        ctx = max(1, block_size * (i % 3 + 1) - (i % block_size))
+        need = (ctx + block_size - 1) // block_size
+        tables.append([(used + j * 7) % n_blocks for j in range(need)])
+        used += need
+        lens.append(ctx)
+    q = torch.randn(n_seqs, n_q, D, dtype=torch.float16, device="cuda")
+    got = paged_attention_decode_batched(q, cache, tables, lens, 1.0 / math.sqrt(D))
+    _check(got, _oracle_decode(cache, q, tables, lens, 1.0 / math.sqrt(D)), torch.float16)
+    raw = paged_attention_decode_hip(q, cache.k_cache, cache.v_cache, tables, lens)
+    assert torch.equal(raw, got)
+
+
+def test_decode_is_order_invariant_bitwise():
+    """reference tests/parity/test_triton_parity.py:89-112, but bit-exact."""
+    torch.manual_seed(1)
+    cache = PagedKVCache(64, 16, 2, 64, dtype=torch.float16, device="cuda")
+    cache.k_cache.normal_()
+    cache.v_cache.normal_()
+    tables, lens = [[0, 1], [5, 2, 9], [3]], [20, 40, 7]
+    q = torch.randn(3, 4, 64, dtype=torch.float16, device="cuda")
+    fwd = paged_attention_decode_batched(q, cache, tables, lens)
+    order = [2, 0, 1]
+    rev = paged_attention_decode_batched(q[order], cache, [tables[i] for i in order],
+                                         [lens[i] for i in order])
+    assert torch.equal(rev, fwd[order])
+    _check(fwd, _oracle_decode(cache, q, tables, lens), torch.float16)
+
+
+def test_single_token_context():
+    """reference tests/parity/test_triton_parity.py:115-124."""
+    torch.manual_seed(2)
+    cache = PagedKVCache(16, 16, 1, 64, dtype=torch.float16, device="cuda")
+    cache.k_cache.normal_()
+    cache.v_cache.normal_()
+    q = torch.randn(1, 1, 64, dtype=torch.float16, device="cuda")
+    got = paged_attention_decode_batched(q, cache, [[0]], [1])
+    # one key: the output is that key's value row exactly
+    assert torch.equal(got[0, 0], cache.v_cache[0, 0, 0])
+
+
+def test_config1_toy_decode_fp32():
+    """Config 1: fp32, batch 4, Hq 4 / Hkv 2, D 64, bs 16, ctx U[17,100],
+    blocks a seeded permutation of a 64-block pool."""
+    rng = np.random.default_rng(0)
+    gen = torch.Generator().manual_seed(0)
+    lens = [int(x) for x in rng.integers(17, 101, size=4)]
+    cache = PagedKVCache(64, 16, 2, 64, dtype=torch.float32, device="cuda")
+    fill_cache(cache, gen)
+    tables = ragged_tables(rng, lens, 16, 64)
+    q = torch.randn(4, 4, 64, generator=gen).to(dev())
+    got = paged_attention_decode_batched(q, cache, tables, lens, 1.0 / 8)
+    want = _oracle_decode(cache, q, tables, lens, 1.0 / 8)
+    _check(got, want, torch.float32, "cfg1")
+    # and the reference's own dense oracle per sequence
+    for i, (t, c) in enumerate(zip(tables, lens)):
+        k, v = pool_of(cache).gather(t, c)
+        np.testing.assert_allclose(to_np(got[i]), R.attention_decode(to_np(q[i]), k, v, 1 / 8),
+                                   atol=2e-5)
+
+
+@pytest.mark.parametrize("D", [8, 16, 32, 64, 128, 256])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_head_dims_and_dtypes(D, dtype):
+    lens = [1, 15, 16, 17, 33, 100, 257]
+    cache, tables, q = _case(10 + D, len(lens), lens, 4, 2, D, 16, dtype)
+    got = paged_attention_decode_batched(q, cache, tables, lens)
+    _check(got, _oracle_decode(cache, q, tables, lens), dtype, f"D={D} {dtype}")
+
+
+@pytest.mark.parametrize("scale_dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_int8_kv(scale_dtype, D, dtype):
+    lens = [3, 16, 31, 64, 200, 513]
+    cache, tables, q = _case(20 + D, len(lens), lens, 8, 2, D, 16, dtype, quant=True,
+                             scale_dtype=scale_dtype)
+    got = paged_attention_decode_batched(q, cache, tables, lens)
+    _check(got, _oracle_decode(cache, q, tables, lens), dtype, f"int8 D={D}")
+
+
+@pytest.mark.parametrize("Hq,Hkv,T", [(32, 8, 3), (14, 2, 1), (14, 2, 3), (8, 1, 5), (16, 1, 4), (2, 2, 2)])
+@pytest.mark.parametrize("quant", [False, True])
+def test_verify_rows_and_gqa_groups(Hq, Hkv, T, quant):
+    """Multi-token verify (q_per_seq = T, causal among the T tokens) over
+    every row-tile width (G*T up to 64)."""
+    lens = [T, T + 5, 40, 129, 300]
+    cache, tables, q = _case(30 + Hq + T, len(lens), lens, Hq, Hkv, 128, 16, torch.float16,
+                             quant=quant, q_per_seq=T)
+    got = paged_attention_verify_batched(q, cache, tables, lens, T)
+    want = _oracle_decode(cache, q, tables, lens, q_per_seq=T)
+    _check(got, want, torch.float16, f"verify {Hq}/{Hkv}x{T}")
+
+
+@pytest.mark.parametrize("part", [128, 256, 512])
+def test_split_k_long_contexts(part):
+    """Contexts spanning many partitions (split-K + merge), including
+    lengths that end mid-step and mid-partition."""
+    lens = [1, 127, 128, 129, 1000, 4096, 5001]
+    cache, tables, q = _case(40 + part, len(lens), lens, 14, 2, 64, 16, torch.float16)
+    k, v = cache.k_cache, cache.v_cache
+    got = paged_attention_decode_hip(q, k, v, tables, lens, part_tokens=part)
+    _check(got, _oracle_decode(cache, q, tables, lens), torch.float16, f"part {part}")
+    # the partition size changes the summation order only
+    other = paged_attention_decode_hip(q, k, v, tables, lens, part_tokens=1024)
+    assert max_abs(to_np(got), to_np(other)) <= 2e-3
+
+
+def test_split_k_int8_verify():
+    lens = [2000, 3, 4500, 777]
+    cache, tables, q = _case(50, len(lens), lens, 32, 8, 128, 16, torch.float16, quant=True,
+                             q_per_seq=3)
+    got = paged_attention_decode_hip(q, cache.k_cache, cache.v_cache, tables, lens,
+                                     k_scale=cache.k_scale, v_scale=cache.v_scale, q_per_seq=3,
+                                     part_tokens=256)
+    _check(got, _oracle_decode(cache, q, tables, lens, q_per_seq=3), torch.float16)
+
+
+def test_block_size_4_and_non_contiguous_tables():
+    """reference tests/parity/test_parity.py uses 4-token blocks."""
+    lens = [1, 4, 5, 11, 33, 70]
+    cache, tables, q = _case(60, len(lens), lens, 4, 2, 32, 4, torch.float32)
+    got = paged_attention_decode_batched(q, cache, tables, lens)
+    _check(got, _oracle_decode(cache, q, tables, lens), torch.float32)
+
+
+def test_single_sequence_api_and_empty_context():
+    cache, tables, q = _case(70, 1, [45], 4, 2, 64, 16, torch.float16)
+    got = paged_attention_decode(q[0], cache, tables[0], 45)
+    _check(got[None], _oracle_decode(cache, q, tables, [45]), torch.float16)
+    # an empty context is defined as zeros (helios would give NaN)
+    z = paged_attention_decode_batched(q, cache, tables, [0])
+    assert torch.count_nonzero(z) == 0
+
+
+def test_device_tensor_tables_match_list_tables():
+    lens = [50, 700, 3]
+    cache, tables, q = _case(80, 3, lens, 8, 2, 64, 16, torch.float16)
+    width = max(len(t) for t in tables)
+    tt = torch.tensor([t + [0] * (width - len(t)) for t in tables], dtype=torch.int32, device="cuda")
+    lt = torch.tensor(lens, dtype=torch.int32, device="cuda")
+    a = paged_attention_decode_hip(q, cache.k_cache, cache.v_cache, tables, lens)
+    b = paged_attention_decode_hip(q, cache.k_cache, cache.v_cache, tt, lt, max_context_len=700)
+    assert torch.equal(a, b)
