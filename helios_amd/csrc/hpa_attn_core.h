@@ -316,10 +316,27 @@ struct AttnCore {
       l[nt] = l[nt] * alpha + psum;
       Frag<CT> pf;
       frag_from_f32(pf, x);
+      if constexpr (std::is_same<CT, BF16>::value) {
+        // bf16 keeps 8 significant bits; P = hi + lo with both halves in
+        // bf16 carries ~16, so probabilities are not the error term.
+        float lo[8];
 #pragma unroll
-      for (int j = 0; j < J; ++j) {
-        o[nt][j] = o[nt][j] * alpha;
-        o[nt][j] = mma(vf[j], pf, o[nt][j]);
+        for (int s = 0; s < 8; ++s)
+          lo[s] = x[s] - bf16_bits_to_f32((pf.w[s >> 1] >> (16 * (s & 1))) & 0xffffu);
+        Frag<CT> pl;
+        frag_from_f32(pl, lo);
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+          o[nt][j] = o[nt][j] * alpha;
+          o[nt][j] = mma(vf[j], pf, o[nt][j]);
+          o[nt][j] = mma(vf[j], pl, o[nt][j]);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+          o[nt][j] = o[nt][j] * alpha;
+          o[nt][j] = mma(vf[j], pf, o[nt][j]);
+        }
       }
     }
   }

@@ -21,15 +21,17 @@ def to_np(t: torch.Tensor) -> np.ndarray:
     return t.cpu().numpy()
 
 
-def fill_cache(cache, gen: torch.Generator, scale_range=(0.005, 0.05)):
-    """Random pool contents: N(0,1) for fp pools, uniform int8 and positive
-    scales for int8 pools (independent of the write kernel)."""
+def fill_cache(cache, gen: torch.Generator):
+    """Random pool contents: N(0,1) for fp pools; for int8 pools, N(0,1) fp16
+    values quantized by the oracle (the configs' recipe), so the attention
+    tests do not depend on the write kernel."""
     if cache.k_cache.dtype == torch.int8:
-        for t in (cache.k_cache, cache.v_cache):
-            t.copy_(torch.randint(-127, 128, t.shape, generator=gen, device="cpu", dtype=torch.int8))
-        lo, hi = scale_range
-        for s in (cache.k_scale, cache.v_scale):
-            s.copy_((torch.rand(s.shape, generator=gen) * (hi - lo) + lo).to(s.dtype))
+        sdt = np.float16 if cache.k_scale.dtype == torch.float16 else np.float32
+        for t, s in ((cache.k_cache, cache.k_scale), (cache.v_cache, cache.v_scale)):
+            x = torch.randn(t.shape, generator=gen).half().float().numpy()
+            q, sc = R.quantize(x)
+            t.copy_(torch.from_numpy(q))
+            s.copy_(torch.from_numpy(R.store_scale(sc, sdt)))
     else:
         for t in (cache.k_cache, cache.v_cache):
             t.copy_(torch.randn(t.shape, generator=gen).to(t.dtype))

@@ -4,8 +4,8 @@ the oracle, on seeded inputs.
 Tolerances (stated by the build's target): fp16 output max-abs <= 2e-3 against
 a float64 reference computed from the same rounded inputs (int8 values
 dequantised with the stored scales); bf16 gets one bf16 half-ulp of the
-reference on top (output rounding alone nearly fills 2e-3 there); fp32 KV
-(the toy-model path) <= 2e-5.  Batch-order invariance is asserted bit-exact.
+reference (|ref| * 2^-8) on top, since rounding the output to bf16 alone
+exceeds 2e-3 once |out| > 0.5; fp32 KV (the toy-model path) <= 2e-5.  Batch-order invariance is asserted bit-exact.
 """
 
 from __future__ import annotations
@@ -35,7 +35,7 @@ TOL = {torch.float16: 2e-3, torch.bfloat16: 2e-3, torch.float32: 2e-5}
 def _tol(dtype, want):
     t = TOL[dtype]
     if dtype == torch.bfloat16:
-        return t + np.abs(want) * 2.0 ** -9
+        return t + np.abs(want) * 2.0 ** -8
     return t
 
 
