@@ -1,0 +1,418 @@
+#!/usr/bin/env python3
+"""Benchmark of helios' paged-attention hot path on one MI355X.
+
+One "step" is one call of the hot path over one batch of seeded synthetic
+input already resident in HBM.  The default workload is config 5 of
+BASELINE.json -- Llama-3-8B-shape INT8-KV decode + speculative verify
+(Hq 32 / Hkv 8, D 128, batch 256, 3 query tokens per sequence, contexts
+lognormal(median 2048, sigma 0.5) clipped to [64, 32768], block size 16),
+the shape the build's >= 70%-of-HBM target is stated on.  ``--config N``
+measures the other configs the same way.
+
+Prints ONE JSON line (the driver's contract) with a ``roofline`` object for
+the dominant kernel and a ``cpu_baseline`` object: the oracle's restatement of
+helios' own CPU route, timed on a bounded sample on this host.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, 8 TB/s
+MFMA_F16_PEAK_TFS = 2500.0  # MI355X dense fp16/bf16 MFMA, 2.5 PFLOP/s
+BLOCK = 16
+
+
+def _ctx_lognormal(rng, n, median, sigma, lo, hi):
+    import numpy as np
+
+    x = np.exp(rng.normal(math.log(median), sigma, size=n))
+    return [int(v) for v in np.clip(np.rint(x), lo, hi)]
+
+
+class Workload:
+    """A seeded config: device tensors, the step to time, and its work."""
+
+    name = ""
+    bound = "hbm"
+
+    def step(self):  # pragma: no cover - overridden
+        raise NotImplementedError
+
+
+def _shuffled_tables(rng, lens, device):
+    import numpy as np
+    import torch
+
+    need = [(c + BLOCK - 1) // BLOCK for c in lens]
+    nb = int(sum(need))
+    perm = rng.permutation(nb).astype(np.int32)
+    width = max(need)
+    tab = np.zeros((len(lens), width), np.int32)
+    o = 0
+    for i, n in enumerate(need):
+        tab[i, :n] = perm[o:o + n]
+        o += n
+    return nb, torch.from_numpy(tab).to(device), tab
+
+
+def _fill_by_writes(cache, lens, tables_t, gen, device, chunk_tokens=1 << 19):
+    """Fill every (sequence, position) of the pool with N(0,1) fp16 K/V through
+    the library's own write kernel (for int8 pools: quantize + scatter, the
+    configs' 'quantized N(0,1) fp16' recipe)."""
+    import torch
+
+    from helios_amd import write_kv
+
+    H, D = cache.n_kv_heads, cache.head_dim
+    i = 0
+    while i < len(lens):
+        j, tok = i, 0
+        while j < len(lens) and (tok == 0 or tok + lens[j] <= chunk_tokens):
+            tok += lens[j]
+            j += 1
+        k = torch.randn(tok, H, D, generator=gen, device=device, dtype=torch.float16)
+        v = torch.randn(tok, H, D, generator=gen, device=device, dtype=torch.float16)
+        write_kv(cache, tables_t[i:j], [0] * (j - i), k, v, query_lens=lens[i:j])
+        i = j
+    torch.cuda.synchronize()
+
+
+class DecodeWorkload(Workload):
+    """Configs 2, 3 and 5: batched decode (q_per_seq 1) or verify (3)."""
+
+    def __init__(self, cfg, device, seed, part_tokens=0, copies=1):
+        import numpy as np
+        import torch
+
+        import helios_amd as H
+
+        self.cfg = cfg
+        rng = np.random.default_rng(seed)
+        gen = torch.Generator(device=device).manual_seed(seed)
+        if cfg == 5:
+            self.name = "llama3-8b-int8-decode-verify (config 5)"
+            B, Hq, Hkv, D, Tq, quant = 256, 32, 8, 128, 3, True
+            lens = _ctx_lognormal(rng, B, 2048, 0.5, 64, 32768)
+        elif cfg in (2, 3):
+            quant = cfg == 3
+            self.name = ("qwen2.5-0.5b-int8-decode+write (config 3)" if quant
+                         else "qwen2.5-0.5b-fp16-decode (config 2)")
+            B, Hq, Hkv, D, Tq = 64, 14, 2, 64, 1
+            lens = [int(x) for x in rng.integers(512, 4097, size=B)]
+        else:
+            self.name = "toy-fp32-decode (config 1)"
+            B, Hq, Hkv, D, Tq, quant = 4, 4, 2, 64, 1, False
+            lens = [int(x) for x in rng.integers(17, 101, size=B)]
+        dtype = torch.float32 if cfg == 1 else torch.float16
+        self.B, self.Hq, self.Hkv, self.D, self.Tq, self.quant = B, Hq, Hkv, D, Tq, quant
+        self.lens = lens
+        nb, self.tables_t, self.tables_np = _shuffled_tables(rng, lens, device)
+        self.lens_t = torch.tensor(lens, dtype=torch.int32, device=device)
+        self.max_ctx = max(lens)
+        self.scale = 1.0 / math.sqrt(D)
+        self.part_tokens = part_tokens
+        # Configs 2/3 fit in the 256 MB Infinity Cache: rotate over enough
+        # pool copies that every step reads from HBM.
+        self.caches = []
+        for _ in range(copies):
+            if quant:
+                c = H.QuantizedPagedKVCache(nb, BLOCK, Hkv, D, dtype=dtype, device=device,
+                                            scale_dtype=torch.float16)
+            else:
+                c = H.PagedKVCache(nb, BLOCK, Hkv, D, dtype=dtype, device=device)
+            _fill_by_writes(c, lens, self.tables_t, gen, device)
+            self.caches.append(c)
+        self.q = torch.randn(B * Tq, Hq, D, generator=gen, device=device, dtype=dtype)
+        self.out = torch.empty_like(self.q)
+        ws = H.decode_workspace_bytes(B, Tq, Hq, Hkv, D, self.max_ctx, part_tokens)
+        self.ws = torch.empty(max(ws, 1), dtype=torch.uint8, device=device)
+        if cfg == 3:  # one new token per sequence, written at position ctx - 1
+            self.new_k = torch.randn(B, Hkv, D, generator=gen, device=device, dtype=dtype)
+            self.new_v = torch.randn(B, Hkv, D, generator=gen, device=device, dtype=dtype)
+            self.new_pos = torch.tensor([c - 1 for c in lens], dtype=torch.int32, device=device)
+            self.ones = [1] * B
+        self.i = 0
+        kvb = D * (1 if quant else (4 if cfg == 1 else 2)) + (2 if quant else 0)
+        elt = 4 if cfg == 1 else 2
+        sum_ctx = sum(lens)
+        n_tab = sum((c + BLOCK - 1) // BLOCK for c in lens)
+        self.kv_bytes = sum_ctx * 2 * Hkv * kvb
+        self.alg_bytes = self.kv_bytes + 2 * B * Tq * Hq * D * elt + 4 * n_tab + 4 * B
+        if cfg == 3:  # the write: read K,V fp16, write int8 + fp16 scale
+            self.alg_bytes += B * 2 * Hkv * (D * 2 + D + 2)
+        self.flops = 4 * D * Hq * sum(sum(min(c, c - Tq + t + 1) for t in range(Tq)) for c in lens)
+        self.tokens = B * Tq
+
+    def step(self):
+        import helios_amd as H
+
+        c = self.caches[self.i % len(self.caches)]
+        self.i += 1
+        if self.cfg == 3:
+            H.write_kv(c, self.tables_t, self.new_pos, self.new_k, self.new_v, query_lens=self.ones)
+        ks, vs = c._scales()
+        H.paged_attention_decode_hip(
+            self.q, c.k_cache, c.v_cache, self.tables_t, self.lens_t, self.scale, ks, vs,
+            q_per_seq=self.Tq, max_context_len=self.max_ctx, part_tokens=self.part_tokens,
+            out=self.out, workspace=self.ws,
+        )
+
+    def config(self):
+        return {"workload": self.name, "batch": self.B, "q_per_seq": self.Tq,
+                "n_q_heads": self.Hq, "n_kv_heads": self.Hkv, "head_dim": self.D,
+                "block_size": BLOCK, "kv_dtype": "int8" if self.quant else
+                ("fp32" if self.cfg == 1 else "fp16"),
+                "scale_dtype": "fp16" if self.quant else None,
+                "context": {"mean": round(sum(self.lens) / len(self.lens), 1),
+                            "max": self.max_ctx, "min": min(self.lens)},
+                "pool_copies": len(self.caches), "part_tokens": self.part_tokens or "auto"}
+
+    def cpu_baseline(self, budget_s):
+        """helios' CPU route (fp32, reference engine.py:135-138) on a bounded
+        sample: decode -> paged_attention_decode_batched; verify -> one
+        paged_attention_prefill per sequence (reference runner.py:354-362)."""
+        import numpy as np
+
+        from oracle import paged_ref as R
+
+        c = self.caches[0]
+        pool = R.PagedPool(c.num_blocks, BLOCK, self.Hkv, self.D, np.float32, quantized=self.quant)
+        pool.k = c.k_cache.cpu().numpy()
+        pool.v = c.v_cache.cpu().numpy()
+        if self.quant:
+            pool.k_scale = c.k_scale.cpu().numpy()
+            pool.v_scale = c.v_scale.cpu().numpy()
+        else:
+            pool.k = pool.k.astype(np.float32)
+            pool.v = pool.v.astype(np.float32)
+        q = self.q.float().cpu().numpy()
+        tabs = [list(self.tables_np[i, :(n + BLOCK - 1) // BLOCK]) for i, n in enumerate(self.lens)]
+        done, t0 = 0, time.perf_counter()
+        if self.Tq == 1:
+            chunk = 8
+            while done < self.B and time.perf_counter() - t0 < budget_s:
+                sl = slice(done, min(self.B, done + chunk))
+                R.helios_cpu_decode_batched_fp32(q[sl], pool, tabs[sl], self.lens[sl], self.scale)
+                done = sl.stop
+        else:
+            T = self.Tq
+            while done < self.B and time.perf_counter() - t0 < budget_s:
+                c_ = self.lens[done]
+                R.helios_cpu_prefill_fp32(q[done * T:(done + 1) * T], pool, tabs[done], c_ - T, c_,
+                                          self.scale)
+                done += 1
+        dt = time.perf_counter() - t0
+        return done * self.Tq, dt, f"{done} of {self.B} sequences ({done * self.Tq} query tokens)"
+
+
+class PrefillWorkload(Workload):
+    """Config 4: 8 sequences each appending a 512-token chunk onto prior
+    context U[0, 3584]; the first 64 blocks (1024 tokens) of every table are
+    the same physical blocks wherever the prior context covers them."""
+
+    bound = "mfma"
+
+    def __init__(self, device, seed):
+        import numpy as np
+        import torch
+
+        import helios_amd as H
+
+        self.name = "llama3-8b-fp16-chunked-prefill (config 4)"
+        rng = np.random.default_rng(seed)
+        gen = torch.Generator(device=device).manual_seed(seed)
+        B, Hq, Hkv, D, T = 8, 32, 8, 128, 512
+        self.B, self.Hq, self.Hkv, self.D, self.T = B, Hq, Hkv, D, T
+        priors = [int(x) for x in rng.integers(0, 3585, size=B)]
+        ctxs = [p + T for p in priors]
+        shared = 64
+        need = [(c + BLOCK - 1) // BLOCK for c in ctxs]
+        own_shared = [min(shared, p // BLOCK) for p in priors]  # only full prior blocks alias
+        nb = shared + sum(n - s for n, s in zip(need, own_shared))
+        perm = [int(x) for x in rng.permutation(nb)]
+        prefix, rest = perm[:shared], perm[shared:]
+        tabs, o = [], 0
+        for n, s in zip(need, own_shared):
+            tabs.append(prefix[:s] + rest[o:o + n - s])
+            o += n - s
+        width = max(need)
+        tab = np.zeros((B, width), np.int32)
+        for i, t in enumerate(tabs):
+            tab[i, :len(t)] = t
+        self.tables_t = torch.from_numpy(tab).to(device)
+        self.tabs = tabs
+        self.priors, self.ctxs = priors, ctxs
+        self.cache = H.PagedKVCache(nb, BLOCK, Hkv, D, dtype=torch.float16, device=device)
+        for t in (self.cache.k_cache, self.cache.v_cache):
+            t.normal_(generator=gen)
+        self.q = torch.randn(B * T, Hq, D, generator=gen, device=device, dtype=torch.float16)
+        self.qlens = torch.full((B,), T, dtype=torch.int32, device=device)
+        self.pos_t = torch.tensor(priors, dtype=torch.int32, device=device)
+        self.ctx_t = torch.tensor(ctxs, dtype=torch.int32, device=device)
+        self.scale = 1.0 / math.sqrt(D)
+        self.flops = 4 * D * Hq * sum(sum(p + i + 1 for i in range(T)) for p in priors)
+        n_tab = sum(need)
+        self.alg_bytes = sum(ctxs) * 2 * Hkv * D * 2 + 2 * B * T * Hq * D * 2 + 4 * n_tab
+        self.tokens = B * T
+
+    def step(self):
+        import helios_amd as H
+
+        H.paged_attention_varlen(self.q, self.cache, self.tables_t, self.qlens, self.pos_t,
+                                 self.ctx_t, self.scale, max_query_len=self.T)
+
+    def config(self):
+        return {"workload": self.name, "sequences": self.B, "chunk": self.T,
+                "n_q_heads": self.Hq, "n_kv_heads": self.Hkv, "head_dim": self.D,
+                "block_size": BLOCK, "kv_dtype": "fp16", "prior_context": self.priors,
+                "shared_prefix_blocks": 64}
+
+    def cpu_baseline(self, budget_s):
+        import numpy as np
+
+        from oracle import paged_ref as R
+
+        pool = R.PagedPool(self.cache.num_blocks, BLOCK, self.Hkv, self.D, np.float32)
+        pool.k = self.cache.k_cache.float().cpu().numpy()
+        pool.v = self.cache.v_cache.float().cpu().numpy()
+        q = self.q.float().cpu().numpy()
+        done, t0 = 0, time.perf_counter()
+        while done < self.B and time.perf_counter() - t0 < budget_s:
+            R.helios_cpu_prefill_fp32(q[done * self.T:(done + 1) * self.T], pool, self.tabs[done],
+                                      self.priors[done], self.ctxs[done], self.scale)
+            done += 1
+        dt = time.perf_counter() - t0
+        return done * self.T, dt, f"{done} of {self.B} sequences ({done * self.T} query tokens)"
+
+
+def _cpu_threads():
+    try:
+        from threadpoolctl import threadpool_info
+
+        n = [i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"]
+        if n:
+            return int(max(n))
+    except Exception:
+        pass
+    return len(os.sched_getaffinity(0))
+
+
+def _traffic(workload_key):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary, if any."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{workload_key}.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("bytes_per_launch")
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", type=int, default=5, choices=[1, 2, 3, 4, 5])
+    ap.add_argument("--seed", type=int, default=None)
+    ap.add_argument("--part-tokens", type=int, default=0,
+                    help="split-K partition size for decode (0 = library default)")
+    ap.add_argument("--copies", type=int, default=None,
+                    help="pool copies rotated per step (default: enough to exceed 256 MB)")
+    ap.add_argument("--cpu-budget", type=float, default=15.0,
+                    help="seconds of CPU baseline work (0 disables it)")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(json.dumps({"error": "this build runs on one GPU only: the paged-attention path "
+                                   "has no multi-GPU mode (see DESIGN.md, sharding)",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+
+    import torch
+
+    import helios_amd  # noqa: F401
+
+    if not torch.cuda.is_available():
+        raise SystemExit("bench.py needs a GPU")
+    device = torch.device("cuda:0")
+    seed = args.config - 1 if args.seed is None else args.seed
+
+    if args.config == 4:
+        wl = PrefillWorkload(device, seed)
+    else:
+        copies = args.copies
+        if copies is None:
+            copies = 1 if args.config in (1, 5) else 5
+        wl = DecodeWorkload(args.config, device, seed, args.part_tokens, copies)
+
+    for _ in range(args.warmup):
+        wl.step()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    t_wall = time.perf_counter()
+    start.record()
+    for _ in range(args.steps):
+        wl.step()
+    end.record()
+    end.synchronize()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_wall
+    ms = start.elapsed_time(end) / args.steps
+
+    value = wl.tokens / (ms * 1e-3)
+    if wl.bound == "hbm":
+        achieved = wl.alg_bytes / (ms * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": _traffic(f"config{args.config}"),
+                "algorithmic_bytes": int(wl.alg_bytes)}
+    else:
+        achieved = wl.flops / (ms * 1e-3) / 1e12
+        roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_F16_PEAK_TFS,
+                "unit": "TFLOP/s", "frac": round(achieved / MFMA_F16_PEAK_TFS, 4),
+                "traffic": _traffic(f"config{args.config}"),
+                "algorithmic_flops": int(wl.flops)}
+    roof["kernel"] = "decode_kernel + decode_reduce_kernel" if wl.bound == "hbm" else "prefill_kernel"
+
+    cpu = None
+    if args.cpu_budget > 0:
+        tokens, secs, sample = wl.cpu_baseline(args.cpu_budget)
+        cpu = {"value": round(tokens / secs, 1) if secs > 0 else None, "unit": "tokens/s",
+               "cores": _cpu_threads(), "kind": "port", "sample": sample,
+               "seconds": round(secs, 2)}
+
+    line = {
+        "metric": "paged-attn decode tokens/s + achieved HBM GB/s (% peak) on 1 MI355X"
+        if wl.bound == "hbm" else "paged-attn chunked-prefill tokens/s + MFMA TFLOP/s (% peak) on 1 MI355X",
+        "value": round(value, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8-kv/fp16" if getattr(wl, "quant", False) else
+        ("f32" if args.config == 1 else "f16"),
+        "data": "synthetic (seeded N(0,1); int8 KV quantized on the GPU by the library's write kernel)",
+        "config": wl.config(),
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "wall_s_timed_region": round(wall, 4),
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -13,6 +13,7 @@ from .paged_attn import (  # noqa: F401
     _repeat_kv,
     _repeat_kv_batched,
     copy_blocks,
+    decode_workspace_bytes,
     hip_available,
     paged_attention_decode,
     paged_attention_decode_batched,
@@ -27,6 +28,7 @@ __all__ = [
     "PagedKVCache",
     "QuantizedPagedKVCache",
     "copy_blocks",
+    "decode_workspace_bytes",
     "hip_available",
     "paged_attention_decode",
     "paged_attention_decode_batched",

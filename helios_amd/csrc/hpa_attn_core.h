@@ -97,8 +97,19 @@ struct AttnCore {
     uint32_t vs[2][SW];
   };
 
+  // int8 KV with fp16 compute converts a byte x to the fp16 value 1152 + x
+  // (two VALU ops per pair of values instead of three) and removes the
+  // offset algebraically: S = S' - 1152 * sum(q) and O = O' - 1152 * sum(P').
+  static constexpr bool I8F16 = QUANT && std::is_same<CT, F16>::value;
+  static constexpr float kI8Off = 1152.f;
+  // Rescale the accumulators only when a row max grows by more than 2^8;
+  // probabilities then stay below 2^8 relative to the running reference.
+  static constexpr float kLazy = 8.f;
+
   Frag<CT> q[NT][C];
   f32x4 o[NT][J];
+  f32x4 ps[NT];     // I8F16: sum over keys of the fp16 P' fed to the PV MFMAs
+  float qoff[NT];   // I8F16: 1152 * sum_d q[row][d]
   float m[NT], l[NT];
   int lim[NT];
 
@@ -132,6 +143,21 @@ struct AttnCore {
         } else {
           frag_zero(q[nt][c]);
         }
+      }
+      if constexpr (I8F16) {
+        float sq = 0.f;
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            // copy the element out first: a bit_cast applied directly to an
+            // ext_vector element reads element 0 (seen with hipcc 7.2)
+            const uint32_t wi = q[nt][c].w[i];
+            const f16x2 h = __builtin_bit_cast(f16x2, wi);
+            sq += (float)h[0] + (float)h[1];
+          }
+        qoff[nt] = kI8Off * xor_sum(sq);
+        ps[nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
       }
     }
   }
@@ -188,6 +214,74 @@ struct AttnCore {
     }
   }
 
+  // Lane-constant byte offsets of the fast path (block_size >= 16).
+  struct LaneOff {
+    uint32_t k, v, s;
+  };
+  __device__ __forceinline__ static LaneOff lane_off() {
+    const int n = lane() & 15, g = lane() >> 4;
+    LaneOff o;
+    o.k = (uint32_t)(n * D * ESZ + g * KPL * ESZ);
+    o.v = (uint32_t)(4 * g * D * ESZ + J * n * ESZ);
+    o.s = (uint32_t)(4 * g * (QUANT ? (int)sizeof(typename ST::storage) : 0));
+    return o;
+  }
+
+  // Fast path for block_size >= 16: a 16-key tile never leaves its block, so
+  // the block base is one scalar table load and every lane address is that
+  // uniform base plus a 32-bit lane-constant offset.  k0 must be
+  // wave-uniform.  A tile at or past the context reads the tile holding the
+  // last key (real memory; its keys are masked, and the fp V slots of keys
+  // past the context are zeroed in compute()).
+  __device__ __forceinline__ static void load_big(const PoolView& pv, int k0, const LaneOff& lo,
+                                                  Raw& r) {
+    const int n = lane() & 15, g = lane() >> 4;
+    const int bsm = (1 << pv.bs_log2) - 1;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int key0 = k0 + 16 * t;
+      const int keyc = key0 < pv.ctx ? key0 : ((pv.ctx - 1) & ~15);
+      int lb = keyc >> pv.bs_log2;
+      lb = lb < pv.table_stride ? lb : pv.table_stride - 1;
+      int phys = pv.table[lb];
+      phys = (unsigned)phys < (unsigned)pv.num_blocks ? phys : 0;
+      const long slot0 = ((long)(phys * pv.num_kv_heads + pv.kvh) << pv.bs_log2) + (keyc & bsm);
+      const char* kb = reinterpret_cast<const char*>(pv.k) + slot0 * (D * ESZ);
+      const char* vb = reinterpret_cast<const char*>(pv.v) + slot0 * (D * ESZ);
+      if (g * KPL < D) {
+        load_raw<KPL * ESZ>(r.k[t], kb + lo.k);
+      } else {
+#pragma unroll
+        for (int i = 0; i < KW; ++i) r.k[t][i] = 0;
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (J * n < D) {
+          load_raw<VB>(r.v[4 * t + i], vb + lo.v + i * (D * ESZ));
+        } else {
+#pragma unroll
+          for (int w = 0; w < VW; ++w) r.v[4 * t + i][w] = 0;
+        }
+      }
+      if constexpr (QUANT) {
+        typedef typename ST::storage s_t;
+        const char* ksb = reinterpret_cast<const char*>(pv.ks) + slot0 * (long)sizeof(s_t);
+        const char* vsb = reinterpret_cast<const char*>(pv.vs) + slot0 * (long)sizeof(s_t);
+        load_raw<SB>(r.ks[t], ksb + lo.s);
+        load_raw<SB>(r.vs[t], vsb + lo.s);
+      }
+    }
+  }
+
+  __device__ __forceinline__ static void load_any(const PoolView& pv, int k0, const LaneOff& lo,
+                                                  Raw& r) {
+    if (pv.bs_log2 >= 4) {
+      load_big(pv, k0, lo, r);
+    } else {
+      load(pv, k0, r);
+    }
+  }
+
   __device__ __forceinline__ static float scale_at(const uint32_t* w, int i) {
     if constexpr (QUANT) {
       if constexpr (std::is_same<ST, F16>::value) {
@@ -204,10 +298,12 @@ struct AttnCore {
     if constexpr (QUANT) {
       const uint32_t w0 = kr[2 * c], w1 = kr[2 * c + 1];
       if constexpr (std::is_same<CT, F16>::value) {
-        f.w[0] = i8pair_to_f16x2(w0, w0, 0, 1);
-        f.w[1] = i8pair_to_f16x2(w0, w0, 2, 3);
-        f.w[2] = i8pair_to_f16x2(w1, w1, 0, 1);
-        f.w[3] = i8pair_to_f16x2(w1, w1, 2, 3);
+        // [b0^0x80, 0x64, b1^0x80, 0x64] = fp16 (1152 + x0, 1152 + x1)
+        const uint32_t x0 = w0 ^ 0x80808080u, x1 = w1 ^ 0x80808080u;
+        f.w[0] = __builtin_amdgcn_perm(0x64646464u, x0, 0x04010400u);
+        f.w[1] = __builtin_amdgcn_perm(0x64646464u, x0, 0x04030402u);
+        f.w[2] = __builtin_amdgcn_perm(0x64646464u, x1, 0x04010400u);
+        f.w[3] = __builtin_amdgcn_perm(0x64646464u, x1, 0x04030402u);
       } else {
         float x[8];
 #pragma unroll
@@ -229,9 +325,11 @@ struct AttnCore {
   __device__ __forceinline__ static void v_frag(const Raw& r, int j, Frag<CT>& f) {
     if constexpr (QUANT) {
       if constexpr (std::is_same<CT, F16>::value) {
+        // fp16 (1152 + x) pairs; the offset leaves through ps[]
 #pragma unroll
         for (int p = 0; p < 4; ++p)
-          f.w[p] = i8pair_to_f16x2(r.v[2 * p][j >> 2], r.v[2 * p + 1][j >> 2], j & 3, j & 3);
+          f.w[p] = __builtin_amdgcn_perm(r.v[2 * p + 1][j >> 2], r.v[2 * p][j >> 2],
+                                         perm_sel_bytes(j & 3, j & 3)) ^ 0x64806480u;
       } else {
         float x[8];
 #pragma unroll
@@ -262,8 +360,21 @@ struct AttnCore {
 
   // One 32-key step. `masked` must be true whenever any key of the step may
   // lie at or beyond some row's limit.
-  __device__ __forceinline__ void compute(const Raw& r, int k0, float scale_log2, bool masked) {
+  __device__ __forceinline__ void compute(Raw& r, int k0, float scale_log2, bool masked, int ctx) {
     const int g = lane() >> 4;
+    if constexpr (!QUANT) {
+      // fp pools may hold NaN in slots never written; P = 0 there must stay 0
+      if (masked) {
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+          const int key = k0 + 16 * (s >> 2) + 4 * g + (s & 3);
+          if (key >= ctx) {
+#pragma unroll
+            for (int w = 0; w < VW; ++w) r.v[s][w] = 0;
+          }
+        }
+      }
+    }
     f32x4 st[2][NT];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
@@ -292,7 +403,9 @@ struct AttnCore {
       float mx = -INFINITY;
 #pragma unroll
       for (int s = 0; s < 8; ++s) {
-        float v = st[s >> 2][nt][s & 3] * ksl[s];
+        float v = st[s >> 2][nt][s & 3];
+        if constexpr (I8F16) v -= qoff[nt];
+        v *= ksl[s];
         if (masked) {
           const int key = k0 + 16 * (s >> 2) + 4 * g + (s & 3);
           v = key < lim[nt] ? v : -INFINITY;
@@ -301,10 +414,19 @@ struct AttnCore {
         mx = fmaxf(mx, v);
       }
       mx = xor_max(mx);
-      const float mnew = fmaxf(m[nt], mx);
-      const float mref = mnew == -INFINITY ? 0.f : mnew;
-      const float alpha = __builtin_amdgcn_exp2f(m[nt] - mref);
-      m[nt] = mnew;
+      // lazy rescale: wave-uniform branch, taken when some row's max grew
+      // by more than 2^kLazy (always on a row's first finite max)
+      const bool grow = mx > m[nt] + kLazy;
+      if (__builtin_amdgcn_ballot_w64(grow)) {
+        const float mnew = grow ? mx : m[nt];
+        const float alpha = __builtin_amdgcn_exp2f(m[nt] - (mnew == -INFINITY ? 0.f : mnew));
+        m[nt] = mnew;
+        l[nt] *= alpha;
+#pragma unroll
+        for (int j = 0; j < J; ++j) o[nt][j] = o[nt][j] * alpha;
+        if constexpr (I8F16) ps[nt] = ps[nt] * alpha;
+      }
+      const float mref = m[nt] == -INFINITY ? 0.f : m[nt];
       float psum = 0.f;
 #pragma unroll
       for (int s = 0; s < 8; ++s) {
@@ -313,7 +435,7 @@ struct AttnCore {
         // a masked key contributes exactly 0, whatever its (unwritten) scale holds
         x[s] = (!masked || x[s] != -INFINITY) ? p * vsc[s] : 0.f;
       }
-      l[nt] = l[nt] * alpha + psum;
+      l[nt] += psum;
       Frag<CT> pf;
       frag_from_f32(pf, x);
       if constexpr (std::is_same<CT, BF16>::value) {
@@ -327,18 +449,25 @@ struct AttnCore {
         frag_from_f32(pl, lo);
 #pragma unroll
         for (int j = 0; j < J; ++j) {
-          o[nt][j] = o[nt][j] * alpha;
           o[nt][j] = mma(vf[j], pf, o[nt][j]);
           o[nt][j] = mma(vf[j], pl, o[nt][j]);
         }
       } else {
 #pragma unroll
-        for (int j = 0; j < J; ++j) {
-          o[nt][j] = o[nt][j] * alpha;
-          o[nt][j] = mma(vf[j], pf, o[nt][j]);
+        for (int j = 0; j < J; ++j) o[nt][j] = mma(vf[j], pf, o[nt][j]);
+        if constexpr (I8F16) {
+          Frag<CT> ones;
+          ones.w = (u32x4){0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u};
+          ps[nt] = mma(ones, pf, ps[nt]);
         }
       }
     }
+  }
+
+  // Accumulator element (j, i) of n-tile nt with the int8 offset removed.
+  __device__ __forceinline__ float out_val(int nt, int j, int i) const {
+    if constexpr (I8F16) return o[nt][j][i] - kI8Off * ps[nt][0];
+    return o[nt][j][i];
   }
 
   // Row total of l for every lane of the row.

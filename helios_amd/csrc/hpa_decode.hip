@@ -57,7 +57,8 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(const DecodeArgs a) {
   const int part = blockIdx.y;
   const int ctx = min(a.ctx_lens[b], a.ctx_cap);
   const int kbeg = part * a.part_tokens;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, n = lane & 15, g = lane >> 4;
+  const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int G = a.group, Tq = a.q_per_seq;
   q_t* out = reinterpret_cast<q_t*>(a.out);
   const q_t* q = reinterpret_cast<const q_t*>(a.q);
@@ -101,15 +102,16 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(const DecodeArgs a) {
               a.num_kv_heads,
               a.bs_log2, a.num_blocks, ctx};
 
+  const typename Core::LaneOff lo = Core::lane_off();
   int k0 = kbeg + 32 * w;
   if (k0 < kend) {
     typename Core::Raw cur;
-    Core::load(pv, k0, cur);
+    Core::load_any(pv, k0, lo, cur);
     for (;;) {
       const int kn = k0 + 32 * NW;
       typename Core::Raw nxt;
-      if (kn < kend) Core::load(pv, kn, nxt);
-      core.compute(cur, k0, a.scale_log2, k0 + 32 > minlim);
+      if (kn < kend) Core::load_any(pv, kn, lo, nxt);
+      core.compute(cur, k0, a.scale_log2, k0 + 32 > minlim, ctx);
       if (kn >= kend) break;
       cur = nxt;
       k0 = kn;
@@ -130,7 +132,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(const DecodeArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int d = Core::out_dim(g, j, i);
-        if (d < D) sm_o[(w * 16 + n) * DS + d] = core.o[nt][j][i];
+        if (d < D) sm_o[(w * 16 + n) * DS + d] = core.out_val(nt, j, i);
       }
     __syncthreads();
     for (int idx = threadIdx.x; idx < 16 * D; idx += 64 * NW) {
@@ -163,11 +165,16 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(const DecodeArgs a) {
 }
 
 // Merges the partition partials of every (sequence, KV head) that has more
-// than one partition, in partition order.
+// than one partition, in partition order (deterministic).  Rows are handled
+// in groups whose weight table fits in LDS: one thread per row computes the
+// row's merged max / sum, then all threads combine the partial outputs with
+// coalesced reads along head_dim.
+constexpr int kReduceLds = 4096;
+
 template <class CT>
 __global__ __launch_bounds__(256) void decode_reduce_kernel(const DecodeArgs a, int D) {
   typedef typename CT::storage q_t;
-  __shared__ float sw[kMaxParts * 2];
+  __shared__ float sw[kReduceLds];
   const int unit = blockIdx.x;
   const int kvh = unit % a.num_kv_heads, b = unit / a.num_kv_heads;
   const int ctx = min(a.ctx_lens[b], a.ctx_cap);
@@ -178,28 +185,30 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(const DecodeArgs a, 
   q_t* out = reinterpret_cast<q_t*>(a.out);
   const float* ml = a.ws_ml + (long)unit * a.max_parts * a.rows * 2;
   const float* po = a.ws_o + (long)unit * a.max_parts * a.rows * D;
-  // one row at a time keeps the weight table at nparts entries
-  for (int r = 0; r < a.rows; ++r) {
-    if (threadIdx.x == 0) {
+  const int rg = max(1, min(a.rows, kReduceLds / nparts));
+  for (int r0 = 0; r0 < a.rows; r0 += rg) {
+    const int nr = min(rg, a.rows - r0);
+    for (int rr = threadIdx.x; rr < nr; rr += 256) {
+      const int r = r0 + rr;
       float M = -INFINITY;
       for (int p = 0; p < nparts; ++p) M = fmaxf(M, ml[2 * (p * a.rows + r)]);
       const float Mref = M == -INFINITY ? 0.f : M;
       float L = 0.f;
       for (int p = 0; p < nparts; ++p) {
         const float wt = __builtin_amdgcn_exp2f(ml[2 * (p * a.rows + r)] - Mref);
-        sw[p] = wt;
+        sw[p * rg + rr] = wt;
         L += wt * ml[2 * (p * a.rows + r) + 1];
       }
-      sw[kMaxParts] = L > 0.f ? 1.f / L : 0.f;
+      const float inv = L > 0.f ? 1.f / L : 0.f;
+      for (int p = 0; p < nparts; ++p) sw[p * rg + rr] *= inv;
     }
     __syncthreads();
-    const float invL = sw[kMaxParts];
-    const int t = r / G, hh = r - t * G;
-    q_t* orow = out + ((long)(b * Tq + t) * a.num_q_heads + kvh * G + hh) * D;
-    for (int d = threadIdx.x; d < D; d += 256) {
+    for (int idx = threadIdx.x; idx < nr * D; idx += 256) {
+      const int rr = idx / D, d = idx - rr * D, r = r0 + rr;
       float O = 0.f;
-      for (int p = 0; p < nparts; ++p) O += sw[p] * po[((long)p * a.rows + r) * D + d];
-      orow[d] = Cvt<CT>::from_f32(O * invL);
+      for (int p = 0; p < nparts; ++p) O += sw[p * rg + rr] * po[((long)p * a.rows + r) * D + d];
+      const int t = r / G, hh = r - t * G;
+      out[((long)(b * Tq + t) * a.num_q_heads + kvh * G + hh) * D + d] = Cvt<CT>::from_f32(O);
     }
     __syncthreads();
   }

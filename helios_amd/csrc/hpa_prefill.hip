@@ -43,7 +43,8 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(const PrefillArgs a) {
   typedef AttnCore<CT, KVT, ST, D, NT> Core;
   typedef typename CT::storage q_t;
   const int b = blockIdx.z, kvh = blockIdx.y;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, n = lane & 15, g = lane >> 4;
+  const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int G = a.group;
   const int q0 = a.cu_q[b];
   const int T = a.cu_q[b + 1] - q0;
@@ -78,15 +79,16 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(const PrefillArgs a) {
               a.num_kv_heads,
               a.bs_log2, a.num_blocks, ctx};
 
+  const typename Core::LaneOff lo = Core::lane_off();
   if (maxlim > 0) {
     int k0 = 0;
     typename Core::Raw cur;
-    Core::load(pv, k0, cur);
+    Core::load_any(pv, k0, lo, cur);
     for (;;) {
       const int kn = k0 + 32;
       typename Core::Raw nxt;
-      if (kn < maxlim) Core::load(pv, kn, nxt);
-      core.compute(cur, k0, a.scale_log2, k0 + 32 > minlim);
+      if (kn < maxlim) Core::load_any(pv, kn, lo, nxt);
+      core.compute(cur, k0, a.scale_log2, k0 + 32 > minlim, ctx);
       if (kn >= maxlim) break;
       cur = nxt;
       k0 = kn;
@@ -105,7 +107,7 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(const PrefillArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int d = Core::out_dim(g, j, i);
-        if (d < D) orow[d] = Cvt<CT>::from_f32(core.o[nt][j][i] * inv);
+        if (d < D) orow[d] = Cvt<CT>::from_f32(core.out_val(nt, j, i) * inv);
       }
   }
 }

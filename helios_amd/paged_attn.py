@@ -344,6 +344,7 @@ def paged_attention_decode_hip(
     max_context_len: Optional[int] = None,
     part_tokens: int = 0,
     out: Optional[torch.Tensor] = None,
+    workspace: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Fused paged decode / verify attention on raw tensors.
 
@@ -355,7 +356,9 @@ def paged_attention_decode_hip(
     sequence with context c attending keys [0, c - q_per_seq + t]).
     ``block_tables`` / ``context_lens`` may be Python lists (converted like
     triton_attn.py:156-165) or int32 device tensors; with tensors pass
-    ``max_context_len`` to avoid a device sync.
+    ``max_context_len`` to avoid a device sync.  ``out`` and ``workspace``
+    (uint8, at least ``decode_workspace_bytes(...)``) may be passed in to keep
+    the call allocation-free.
     """
     _require_gpu(query, "query")
     n_tok, n_q_heads, head_dim = query.shape
@@ -389,7 +392,12 @@ def paged_attention_decode_hip(
     ws_bytes = L.hpa_decode_workspace_size(
         n_seqs, q_per_seq, n_q_heads, n_kv_heads, head_dim, max_context_len, part_tokens
     )
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
+    if workspace is not None:
+        if workspace.numel() * workspace.element_size() < ws_bytes:
+            raise ValueError(f"workspace holds {workspace.nbytes} bytes, {ws_bytes} needed")
+        ws = workspace
+    else:
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
     quant = k_cache.dtype == torch.int8
     st = L.hpa_paged_decode(
         ptr(query), ptr(out), DTYPE_CODE[query.dtype], ptr(k_cache), ptr(v_cache),
@@ -402,6 +410,13 @@ def paged_attention_decode_hip(
     )
     check(st, "hpa_paged_decode")
     return out
+
+
+def decode_workspace_bytes(n_seqs: int, q_per_seq: int, n_q_heads: int, n_kv_heads: int,
+                           head_dim: int, max_context_len: int, part_tokens: int = 0) -> int:
+    """Split-K workspace hpa_paged_decode needs for these shapes."""
+    return int(_lib.load_library().hpa_decode_workspace_size(
+        n_seqs, q_per_seq, n_q_heads, n_kv_heads, head_dim, max_context_len, part_tokens))
 
 
 def _cache_tensors(kv_cache: PagedKVCache):
