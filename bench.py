@@ -135,7 +135,7 @@ class DecodeWorkload(Workload):
         self.q = torch.randn(B * Tq, Hq, D, generator=gen, device=device, dtype=dtype)
         self.out = torch.empty_like(self.q)
         ws = H.decode_workspace_bytes(B, Tq, Hq, Hkv, D, self.max_ctx, part_tokens)
-        self.ws = torch.empty(max(ws, 1), dtype=torch.uint8, device=device)
+        self.ws = torch.zeros(max(ws, 1), dtype=torch.uint8, device=device)
         if cfg == 3:  # one new token per sequence, written at position ctx - 1
             self.new_k = torch.randn(B, Hkv, D, generator=gen, device=device, dtype=dtype)
             self.new_v = torch.randn(B, Hkv, D, generator=gen, device=device, dtype=dtype)

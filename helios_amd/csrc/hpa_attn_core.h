@@ -74,6 +74,30 @@ __device__ __forceinline__ void load_raw(uint32_t* r, const void* p) {
   }
 }
 
+// A window of one sequence's block table held in two VGPRs: lane i holds
+// entries base + i and base + 64 + i.  Block ids are then read with
+// v_readlane at a wave-uniform index, so the KV loads of a step never wait on
+// a table read.  Entries past the table's end read as 0.
+struct TableWindow {
+  int base = 0, limit = 0;  // holds logical blocks [base, limit)
+  uint32_t w0 = 0, w1 = 0;
+
+  __device__ __forceinline__ bool covers(int lb) const { return lb >= base && lb < limit; }
+
+  __device__ __forceinline__ void fill(const int32_t* row, int stride, int b0) {
+    const int lane = threadIdx.x & 63;
+    base = b0;
+    limit = b0 + 128;
+    w0 = b0 + lane < stride ? (uint32_t)row[b0 + lane] : 0u;
+    w1 = b0 + 64 + lane < stride ? (uint32_t)row[b0 + 64 + lane] : 0u;
+  }
+
+  __device__ __forceinline__ int get(int lb) const {
+    const int i = lb - base;
+    return i < 64 ? __builtin_amdgcn_readlane((int)w0, i) : __builtin_amdgcn_readlane((int)w1, i - 64);
+  }
+};
+
 template <class CT, class KVT, class ST, int D, int NT>
 struct AttnCore {
   static constexpr bool QUANT = std::is_same<KVT, I8>::value;
@@ -214,7 +238,8 @@ struct AttnCore {
     }
   }
 
-  // Lane-constant byte offsets of the fast path (block_size >= 16).
+  // Lane-constant byte offsets of the fast path (block_size >= 16), relative
+  // to the first key of a 16-key tile.
   struct LaneOff {
     uint32_t k, v, s;
   };
@@ -228,55 +253,106 @@ struct AttnCore {
   }
 
   // Fast path for block_size >= 16: a 16-key tile never leaves its block, so
-  // the block base is one scalar table load and every lane address is that
-  // uniform base plus a 32-bit lane-constant offset.  k0 must be
-  // wave-uniform.  A tile at or past the context reads the tile holding the
-  // last key (real memory; its keys are masked, and the fp V slots of keys
-  // past the context are zeroed in compute()).
-  __device__ __forceinline__ static void load_big(const PoolView& pv, int k0, const LaneOff& lo,
-                                                  Raw& r) {
-    const int n = lane() & 15, g = lane() >> 4;
-    const int bsm = (1 << pv.bs_log2) - 1;
+  // its four tensors (K, V and, for int8, their scales) are each one
+  // contiguous range whose base is wave-uniform.  Each becomes a buffer
+  // resource (base in SGPRs, lane offsets in one VGPR); a tile wholly past
+  // the context gets a zero-length resource, so its loads return zeros
+  // without touching memory.  The block id comes from the table window held
+  // in registers, so no load waits on a table read.
+  static constexpr int kTileBytes = 16 * D * ESZ;
+  static constexpr int kTileScaleBytes = QUANT ? 16 * (int)sizeof(typename ST::storage) : 0;
+
+  template <int NB>
+  __device__ __forceinline__ static void buf_load(uint32_t* r, __amdgpu_buffer_rsrc_t rs, uint32_t off) {
+    if constexpr (NB >= 16) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int key0 = k0 + 16 * t;
-      const int keyc = key0 < pv.ctx ? key0 : ((pv.ctx - 1) & ~15);
-      int lb = keyc >> pv.bs_log2;
-      lb = lb < pv.table_stride ? lb : pv.table_stride - 1;
-      int phys = pv.table[lb];
-      phys = (unsigned)phys < (unsigned)pv.num_blocks ? phys : 0;
-      const long slot0 = ((long)(phys * pv.num_kv_heads + pv.kvh) << pv.bs_log2) + (keyc & bsm);
-      const char* kb = reinterpret_cast<const char*>(pv.k) + slot0 * (D * ESZ);
-      const char* vb = reinterpret_cast<const char*>(pv.v) + slot0 * (D * ESZ);
-      if (g * KPL < D) {
-        load_raw<KPL * ESZ>(r.k[t], kb + lo.k);
-      } else {
-#pragma unroll
-        for (int i = 0; i < KW; ++i) r.k[t][i] = 0;
+      for (int i = 0; i < NB / 16; ++i) {
+        const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16 * i, 0, 0);
+        r[4 * i + 0] = x[0];
+        r[4 * i + 1] = x[1];
+        r[4 * i + 2] = x[2];
+        r[4 * i + 3] = x[3];
       }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if (J * n < D) {
-          load_raw<VB>(r.v[4 * t + i], vb + lo.v + i * (D * ESZ));
-        } else {
-#pragma unroll
-          for (int w = 0; w < VW; ++w) r.v[4 * t + i][w] = 0;
-        }
-      }
-      if constexpr (QUANT) {
-        typedef typename ST::storage s_t;
-        const char* ksb = reinterpret_cast<const char*>(pv.ks) + slot0 * (long)sizeof(s_t);
-        const char* vsb = reinterpret_cast<const char*>(pv.vs) + slot0 * (long)sizeof(s_t);
-        load_raw<SB>(r.ks[t], ksb + lo.s);
-        load_raw<SB>(r.vs[t], vsb + lo.s);
-      }
+    } else if constexpr (NB == 8) {
+      const u32x2 x = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0);
+      r[0] = x[0];
+      r[1] = x[1];
+    } else if constexpr (NB == 4) {
+      r[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0);
+    } else if constexpr (NB == 2) {
+      r[0] = __builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0);
+    } else {
+      r[0] = __builtin_amdgcn_raw_buffer_load_b8(rs, off, 0, 0);
     }
   }
 
-  __device__ __forceinline__ static void load_any(const PoolView& pv, int k0, const LaneOff& lo,
-                                                  Raw& r) {
-    if (pv.bs_log2 >= 4) {
-      load_big(pv, k0, lo, r);
+  __device__ __forceinline__ static __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int bytes) {
+    // dword 3 = 0x00020000: 32-bit data format, the raw-buffer setting for gfx9 parts
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+  }
+
+  // Loads tile t (keys key0 .. key0 + 15, key0 a multiple of 16) whose block
+  // is `phys`; `valid` false gives zeros.
+  __device__ __forceinline__ static void load_tile(const PoolView& pv, int t, int key0, int phys,
+                                                   bool valid, const LaneOff& lo, Raw& r) {
+    const int n = lane() & 15, g = lane() >> 4;
+    const int bsm = (1 << pv.bs_log2) - 1;
+    const long slot0 = ((long)(phys * pv.num_kv_heads + pv.kvh) << pv.bs_log2) + (key0 & bsm);
+    const char* kb = reinterpret_cast<const char*>(pv.k) + slot0 * (D * ESZ);
+    const char* vb = reinterpret_cast<const char*>(pv.v) + slot0 * (D * ESZ);
+    const int nbytes = valid ? kTileBytes : 0;
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(kb, nbytes);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vb, nbytes);
+    if (g * KPL < D) {
+      buf_load<KPL * ESZ>(r.k[t], rk, lo.k);
+    } else {
+#pragma unroll
+      for (int i = 0; i < KW; ++i) r.k[t][i] = 0;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (J * n < D) {
+        buf_load<VB>(r.v[4 * t + i], rv, lo.v + i * (D * ESZ));
+      } else {
+#pragma unroll
+        for (int w = 0; w < VW; ++w) r.v[4 * t + i][w] = 0;
+      }
+    }
+    if constexpr (QUANT) {
+      typedef typename ST::storage s_t;
+      const int sbytes = valid ? kTileScaleBytes : 0;
+      const __amdgpu_buffer_rsrc_t rks =
+          make_rsrc(reinterpret_cast<const char*>(pv.ks) + slot0 * (long)sizeof(s_t), sbytes);
+      const __amdgpu_buffer_rsrc_t rvs =
+          make_rsrc(reinterpret_cast<const char*>(pv.vs) + slot0 * (long)sizeof(s_t), sbytes);
+      buf_load<SB>(r.ks[t], rks, lo.s);
+      buf_load<SB>(r.vs[t], rvs, lo.s);
+    }
+  }
+
+  // Both tiles of the 32-key step starting at k0 (wave-uniform), fast path.
+  __device__ __forceinline__ static void load_big(const PoolView& pv, TableWindow& win, int k0,
+                                                  const LaneOff& lo, Raw& r) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int key0 = k0 + 16 * t;
+      const bool valid = key0 < pv.ctx;
+      int phys = 0;
+      if (valid) {
+        const int lb = key0 >> pv.bs_log2;
+        if (!win.covers(lb)) win.fill(pv.table, pv.table_stride, lb);
+        phys = win.get(lb);
+        phys = (unsigned)phys < (unsigned)pv.num_blocks ? phys : 0;  // never leave the pool
+      }
+      load_tile(pv, t, key0, phys, valid, lo, r);
+    }
+  }
+
+  template <bool BIG>
+  __device__ __forceinline__ static void load_sel(const PoolView& pv, TableWindow& win, int k0,
+                                                  const LaneOff& lo, Raw& r) {
+    if constexpr (BIG) {
+      load_big(pv, win, k0, lo, r);
     } else {
       load(pv, k0, r);
     }
@@ -349,13 +425,25 @@ struct AttnCore {
     }
   }
 
+  // Reductions over the four 16-lane rows (lanes l, l^16, l^32, l^48) with
+  // the gfx950 row-swap instructions instead of LDS permutes:
+  // permlane16_swap(x, x) yields rows (0,0,2,2) and (1,1,3,3) of x,
+  // permlane32_swap(x, x) yields rows (0,1,0,1) and (2,3,2,3).
   __device__ __forceinline__ static float xor_max(float x) {
-    x = fmaxf(x, __shfl_xor(x, 16));
-    return fmaxf(x, __shfl_xor(x, 32));
+    const uint32_t u = __builtin_bit_cast(uint32_t, x);
+    const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    const float y = fmaxf(__builtin_bit_cast(float, (uint32_t)a[0]), __builtin_bit_cast(float, (uint32_t)a[1]));
+    const uint32_t v = __builtin_bit_cast(uint32_t, y);
+    const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return fmaxf(__builtin_bit_cast(float, (uint32_t)b[0]), __builtin_bit_cast(float, (uint32_t)b[1]));
   }
   __device__ __forceinline__ static float xor_sum(float x) {
-    x += __shfl_xor(x, 16);
-    return x + __shfl_xor(x, 32);
+    const uint32_t u = __builtin_bit_cast(uint32_t, x);
+    const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    const float y = __builtin_bit_cast(float, (uint32_t)a[0]) + __builtin_bit_cast(float, (uint32_t)a[1]);
+    const uint32_t v = __builtin_bit_cast(uint32_t, y);
+    const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return __builtin_bit_cast(float, (uint32_t)b[0]) + __builtin_bit_cast(float, (uint32_t)b[1]);
   }
 
   // One 32-key step. `masked` must be true whenever any key of the step may
@@ -388,15 +476,11 @@ struct AttnCore {
         for (int nt = 0; nt < NT; ++nt) st[t][nt] = mma(kf, q[nt][c], st[t][nt]);
       }
     }
-    float ksl[8], vsc[8];
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      ksl[s] = scale_log2 * scale_at(r.ks[s >> 2], s & 3);
-      vsc[s] = scale_at(r.vs[s >> 2], s & 3);
-    }
-    Frag<CT> vf[J];
-#pragma unroll
-    for (int j = 0; j < J; ++j) v_frag(r, j, vf[j]);
+    // probabilities of every n-tile first, then the PV products one V^T
+    // fragment at a time (each converted once and used by every n-tile), so
+    // at most one converted V fragment is live
+    Frag<CT> pf[NT];
+    Frag<CT> pl[NT];  // bf16 only: the low half of P
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       float x[8];
@@ -405,7 +489,7 @@ struct AttnCore {
       for (int s = 0; s < 8; ++s) {
         float v = st[s >> 2][nt][s & 3];
         if constexpr (I8F16) v -= qoff[nt];
-        v *= ksl[s];
+        v *= scale_log2 * scale_at(r.ks[s >> 2], s & 3);
         if (masked) {
           const int key = k0 + 16 * (s >> 2) + 4 * g + (s & 3);
           v = key < lim[nt] ? v : -INFINITY;
@@ -433,33 +517,33 @@ struct AttnCore {
         const float p = __builtin_amdgcn_exp2f(x[s] - mref);
         psum += p;
         // a masked key contributes exactly 0, whatever its (unwritten) scale holds
-        x[s] = (!masked || x[s] != -INFINITY) ? p * vsc[s] : 0.f;
+        x[s] = (!masked || x[s] != -INFINITY) ? p * scale_at(r.vs[s >> 2], s & 3) : 0.f;
       }
       l[nt] += psum;
-      Frag<CT> pf;
-      frag_from_f32(pf, x);
+      frag_from_f32(pf[nt], x);
       if constexpr (std::is_same<CT, BF16>::value) {
         // bf16 keeps 8 significant bits; P = hi + lo with both halves in
         // bf16 carries ~16, so probabilities are not the error term.
         float lo[8];
 #pragma unroll
         for (int s = 0; s < 8; ++s)
-          lo[s] = x[s] - bf16_bits_to_f32((pf.w[s >> 1] >> (16 * (s & 1))) & 0xffffu);
-        Frag<CT> pl;
-        frag_from_f32(pl, lo);
+          lo[s] = x[s] - bf16_bits_to_f32((pf[nt].w[s >> 1] >> (16 * (s & 1))) & 0xffffu);
+        frag_from_f32(pl[nt], lo);
+      }
+      if constexpr (I8F16) {
+        Frag<CT> ones;
+        ones.w = (u32x4){0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u};
+        ps[nt] = mma(ones, pf[nt], ps[nt]);
+      }
+    }
 #pragma unroll
-        for (int j = 0; j < J; ++j) {
-          o[nt][j] = mma(vf[j], pf, o[nt][j]);
-          o[nt][j] = mma(vf[j], pl, o[nt][j]);
-        }
-      } else {
+    for (int j = 0; j < J; ++j) {
+      Frag<CT> vf;
+      v_frag(r, j, vf);
 #pragma unroll
-        for (int j = 0; j < J; ++j) o[nt][j] = mma(vf[j], pf, o[nt][j]);
-        if constexpr (I8F16) {
-          Frag<CT> ones;
-          ones.w = (u32x4){0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u};
-          ps[nt] = mma(ones, pf, ps[nt]);
-        }
+      for (int nt = 0; nt < NT; ++nt) {
+        o[nt][j] = mma(vf, pf[nt], o[nt][j]);
+        if constexpr (std::is_same<CT, BF16>::value) o[nt][j] = mma(vf, pl[nt], o[nt][j]);
       }
     }
   }

@@ -1,0 +1,6 @@
+// Decode kernels with f32 queries and outputs (see hpa_decode_impl.h).
+#include "hpa_decode_impl.h"
+
+namespace hpa {
+template DecodeFn pick_kv<F32>(int, int, int, int);
+}  // namespace hpa

@@ -1,0 +1,436 @@
+// Paged decode / speculative-verify attention for gfx950.
+//
+// Replaces helios' paged_attention_decode_batched (exec/paged_attn.py:298-353)
+// and the Triton kernel (exec/triton_attn.py:54-130).  Every sequence carries
+// q_per_seq query tokens (1 for decode, gamma+1 for verify); token t of a
+// sequence with context c sits at position c - q_per_seq + t and attends keys
+// [0, c - q_per_seq + t], which is helios' prefill mask (paged_attn.py:401-404)
+// with start_pos = c - q_per_seq.
+//
+// Work decomposition (stream-K).  A "unit" is one (sequence, KV head); it
+// holds ceil(context / 32) steps of 32 keys (one step for an empty context,
+// which writes zeros).  Units are laid end to end, sequence-major, into one
+// global step range of T steps, and the kernel's W waves (as many as the
+// device keeps resident) each take an equal contiguous slice of ceil(T / W)
+// steps.  A wave therefore streams the same number of KV bytes as every other
+// wave whatever the context lengths are, with one step of loads in flight,
+// and pays the unit prologue (block-table window and query rows into
+// registers) only where its slice crosses a unit boundary.  All
+// G * q_per_seq query rows of a KV head live in the wave (GQA packing), so
+// every K/V byte is read from HBM once.
+//
+// A unit that lies wholly inside one wave's slice is normalised and written
+// to `out` by that wave.  A unit cut by slice boundaries is split into
+// pieces held by consecutive waves; each piece leaves its (O, m, l) in the
+// workspace and bumps the unit's arrival counter, and the wave that brings
+// the counter to the piece count merges all pieces in piece order, reading
+// every piece (its own included) back from the workspace, and resets the
+// counter to zero.  The merge order is fixed,
+// so results do not depend on which wave arrives last.  No wave ever waits
+// for another.
+#pragma once
+
+#include <algorithm>
+
+#include "hpa_attn_core.h"
+#include "hpa_host.h"
+
+namespace hpa {
+
+struct DecodeArgs {
+  const void* q;
+  void* out;
+  const void* k;
+  const void* v;
+  const void* ks;
+  const void* vs;
+  const int32_t* tables;
+  int table_stride;
+  const int32_t* ctx_lens;
+  int num_seqs, q_per_seq, num_q_heads, num_kv_heads, group, rows;
+  int bs_log2, num_blocks;
+  float scale_log2;
+  int max_ctx;     // contexts are clamped here
+  int num_waves;   // W: waves launched
+  int min_steps;   // lower bound on a wave's slice, in 32-key steps
+  int* counters;   // [num_seqs * Hkv] arrival counters, zero between calls
+  float* ws_ml;    // [W][2][rows][2]  (m, l) of partial pieces
+  float* ws_o;     // [W][2][rows][D]  unnormalised O of partial pieces
+};
+
+constexpr int kWavesPerGroup = 4;
+constexpr int kWaveCap = 4096;          // 256 CUs x 16 resident waves
+constexpr int kDefaultMinTokens = 256;  // per-wave slice floor (8 steps)
+
+__device__ __forceinline__ int unit_steps(int ctx, int max_ctx) {
+  ctx = min(ctx, max_ctx);
+  return ctx <= 0 ? 1 : (ctx + 31) >> 5;
+}
+
+__device__ __forceinline__ int wave_sum_i(int x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
+__device__ __forceinline__ int wave_incl_scan_i(int x) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o);
+    if (lane >= o) x += y;
+  }
+  return x;
+}
+
+// Position of a wave in the global step range.
+struct UnitPos {
+  int b, kvh;  // unit
+  int n;       // its steps
+  int g;       // global index of its first step
+};
+
+// Steps per KV head summed over all sequences (identical in every wave).
+__device__ int total_steps_per_head(const DecodeArgs& a) {
+  const int lane = threadIdx.x & 63;
+  int acc = 0;
+  for (int base = 0; base < a.num_seqs; base += 256) {
+    int c[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int b = base + 64 * i + lane;
+      c[i] = b < a.num_seqs ? a.ctx_lens[b] : 0;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (base + 64 * i + lane < a.num_seqs) acc += unit_steps(c[i], a.max_ctx);
+  }
+  return wave_sum_i(acc);
+}
+
+// The unit holding global step s0 (< total).  Wave-uniform result.
+__device__ UnitPos locate(const DecodeArgs& a, int s0) {
+  const int lane = threadIdx.x & 63;
+  const int H = a.num_kv_heads;
+  int run = 0;  // steps per head before this chunk
+  UnitPos p{0, 0, 1, 0};
+  for (int base = 0; base < a.num_seqs; base += 64) {
+    const int b = base + lane;
+    const int n = b < a.num_seqs ? unit_steps(a.ctx_lens[b], a.max_ctx) : 0;
+    const int incl = wave_incl_scan_i(n);
+    const int first = H * (run + incl - n);  // global first step of sequence b
+    const int last = H * (run + incl);       // one past its last
+    const unsigned long long hit =
+        __builtin_amdgcn_ballot_w64(b < a.num_seqs && first <= s0 && s0 < last);
+    if (hit) {
+      const int l = __builtin_ffsll((long long)hit) - 1;
+      const int fb = __builtin_amdgcn_readfirstlane(__shfl(first, l));
+      const int nb = __builtin_amdgcn_readfirstlane(__shfl(n, l));
+      p.b = base + l;
+      p.n = nb;
+      p.kvh = (s0 - fb) / nb;
+      p.g = fb + p.kvh * nb;
+      return p;
+    }
+    run += __builtin_amdgcn_readfirstlane(__shfl(incl, 63));
+  }
+  return p;
+}
+
+// Partial pieces travel between waves that may sit on different XCDs, whose
+// L2 caches are not coherent with each other.  They are written and read
+// with device-scope (sc1) buffer accesses, which go through to / come from
+// the device's coherence point, so publishing a piece needs only a wait for
+// its stores to complete, not a device-wide cache write-back.
+constexpr int kCoherent = 16;  // cache-policy bit sc1 (device scope)
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t ws_rsrc(const float* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, 0x7fffffff, 0x00020000);
+}
+
+template <class CT, class KVT, class ST, int D, int NT, bool BIG>
+__global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const DecodeArgs a) {
+  typedef AttnCore<CT, KVT, ST, D, NT> Core;
+  typedef typename CT::storage q_t;
+  constexpr int J = Core::J;
+  const int wave = __builtin_amdgcn_readfirstlane(blockIdx.x * kWavesPerGroup + (threadIdx.x >> 6));
+  if (wave >= a.num_waves) return;
+  const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
+  const int H = a.num_kv_heads, G = a.group, Tq = a.q_per_seq;
+  const q_t* q = reinterpret_cast<const q_t*>(a.q);
+  q_t* out = reinterpret_cast<q_t*>(a.out);
+
+  // ---- this wave's slice [s0, s1) of the global step range
+  const int total = __builtin_amdgcn_readfirstlane(H * total_steps_per_head(a));
+  const int per = max(a.min_steps, (total + a.num_waves - 1) / a.num_waves);
+  const int s0 = wave * per;
+  if (s0 >= total) return;
+  const int s1 = min(total, s0 + per);
+  UnitPos u = locate(a, s0);
+
+  const typename Core::LaneOff lo = Core::lane_off();
+  int ls = s0 - u.g;  // local step inside the unit
+  bool first_unit = true;
+
+  for (;;) {
+    const int ctx = min(__builtin_amdgcn_readfirstlane(a.ctx_lens[u.b]), a.max_ctx);
+    const int lbeg = ls;
+    const int lend = min(u.n, ls + (s1 - (u.g + ls)));  // steps of this unit in the slice
+    const PoolView pv{a.k, a.v, a.ks, a.vs, a.tables + (long)u.b * a.table_stride, a.table_stride,
+                      u.kvh, H, a.bs_log2, a.num_blocks, ctx};
+    TableWindow win;
+    if (BIG && ctx > 0) win.fill(pv.table, pv.table_stride, (32 * lbeg) >> a.bs_log2);
+
+    // ---- unit prologue: query rows of (u.b, u.kvh)
+    auto out_row = [&](int r) -> long {
+      const int t = r / G, hh = r - t * G;
+      return ((long)(u.b * Tq + t) * a.num_q_heads + u.kvh * G + hh) * D;
+    };
+    const q_t* rowq[NT];
+    int rowlim[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int r = nt * 16 + n;
+      if (r < a.rows) {
+        rowq[nt] = q + out_row(r);
+        rowlim[nt] = max(ctx - Tq + r / G + 1, 0);
+      } else {
+        rowq[nt] = nullptr;
+        rowlim[nt] = max(ctx, 0);
+      }
+    }
+    const int minlim = max(ctx - Tq + 1, 0);
+    Core core;
+    core.init(rowq, rowlim);
+
+    // ---- stream the unit's steps [lbeg, lend) with one step in flight
+    if (ctx > 0) {
+      typename Core::Raw cur;
+      Core::template load_sel<BIG>(pv, win, 32 * lbeg, lo, cur);
+      for (int st = lbeg;; ++st) {
+        typename Core::Raw nxt;
+        const bool last = st + 1 >= lend;
+        if (!last) Core::template load_sel<BIG>(pv, win, 32 * (st + 1), lo, nxt);
+        core.compute(cur, 32 * st, a.scale_log2, 32 * st + 32 > minlim, ctx);
+        if (last) break;
+        cur = nxt;
+      }
+    }
+
+    // ---- unit epilogue
+    float lrow[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) lrow[nt] = core.row_l(nt);
+    bool finish = lbeg == 0 && lend == u.n;  // the whole unit is in this slice
+    if (!finish) {
+      // publish this piece, then count it in
+      const long slot = 2L * wave + (first_unit ? 0 : 1);
+      const __amdgpu_buffer_rsrc_t ro = ws_rsrc(a.ws_o), rml = ws_rsrc(a.ws_ml);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const int r = nt * 16 + n;
+        if (r < a.rows) {
+          // the lane's 4J dims are contiguous from 4Jg, element (j, i) at J*i + j
+          float tmp[4 * J];
+#pragma unroll
+          for (int j = 0; j < J; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) tmp[J * i + j] = core.out_val(nt, j, i);
+          const uint32_t ob = (uint32_t)(((slot * a.rows + r) * D + 4 * J * g) * 4);
+#pragma unroll
+          for (int c = 0; c < J; ++c)
+            if (4 * J * g + 4 * c < D)
+              __builtin_amdgcn_raw_buffer_store_b128(
+                  (u32x4){__builtin_bit_cast(uint32_t, tmp[4 * c]), __builtin_bit_cast(uint32_t, tmp[4 * c + 1]),
+                          __builtin_bit_cast(uint32_t, tmp[4 * c + 2]), __builtin_bit_cast(uint32_t, tmp[4 * c + 3])},
+                  ro, ob + 16 * c, 0, kCoherent);
+          if (g == 0)
+            __builtin_amdgcn_raw_buffer_store_b64(
+                (u32x2){__builtin_bit_cast(uint32_t, core.m[nt]), __builtin_bit_cast(uint32_t, lrow[nt])}, rml,
+                (uint32_t)((slot * a.rows + r) * 8), 0, kCoherent);
+        }
+      }
+      const int wa = u.g / per, wb = (u.g + u.n - 1) / per;  // waves holding the pieces
+      const int unit = u.b * H + u.kvh;
+      // the piece's stores are complete (hence visible device-wide) before
+      // the counter moves
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      __builtin_amdgcn_s_waitcnt(0);
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      int old = 0;
+      if (lane == 0) old = __hip_atomic_fetch_add(a.counters + unit, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      old = __builtin_amdgcn_readfirstlane(old);
+      if (old == wb - wa) {
+        // last piece: merge every piece in piece order, all read back from
+        // the workspace (this wave's own included), so every merging wave
+        // evaluates the same expression
+        if (lane == 0) __hip_atomic_store(a.counters + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const long slot_a = 2L * wa + (wa * per == u.g ? 0 : 1);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          const int r = nt * 16 + n;
+          if (r >= a.rows) continue;
+          // running merge over pieces in order: (M, L, acc) rescaled as each
+          // piece's (m, l, O) arrives
+          float M = -INFINITY, L = 0.f;
+          float acc[4 * J];
+#pragma unroll
+          for (int e = 0; e < 4 * J; ++e) acc[e] = 0.f;
+#pragma unroll 2
+          for (int p = wa; p <= wb; ++p) {
+            const long sl = p == wa ? slot_a : 2L * p;
+            const u32x2 ml = __builtin_amdgcn_raw_buffer_load_b64(rml, (uint32_t)((sl * a.rows + r) * 8), 0, kCoherent);
+            const uint32_t ob = (uint32_t)(((sl * a.rows + r) * D + 4 * J * g) * 4);
+            u32x4 ov[J];
+#pragma unroll
+            for (int c = 0; c < J; ++c)
+              ov[c] = 4 * J * g + 4 * c < D
+                          ? __builtin_amdgcn_raw_buffer_load_b128(ro, ob + 16 * c, 0, kCoherent)
+                          : (u32x4){0, 0, 0, 0};
+            // elements are copied out before bit_cast: a bit_cast applied to an
+            // ext_vector element reads element 0 (hipcc 7.2)
+            const uint32_t m0 = ml[0], l0 = ml[1];
+            const float mp = __builtin_bit_cast(float, m0), lp = __builtin_bit_cast(float, l0);
+            const float Mn = fmaxf(M, mp);
+            const float Mref = Mn == -INFINITY ? 0.f : Mn;
+            const float sa = __builtin_amdgcn_exp2f(M - Mref), sb = __builtin_amdgcn_exp2f(mp - Mref);
+            L = L * sa + lp * sb;
+#pragma unroll
+            for (int c = 0; c < J; ++c)
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+              {
+                const uint32_t oe = ov[c][e];
+                acc[4 * c + e] = acc[4 * c + e] * sa + __builtin_bit_cast(float, oe) * sb;
+              }
+            M = Mn;
+          }
+          const float inv = L > 0.f ? 1.f / L : 0.f;
+          q_t* orow = out + out_row(r);
+#pragma unroll
+          for (int j = 0; j < J; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int d = Core::out_dim(g, j, i);
+              if (d < D) orow[d] = Cvt<CT>::from_f32(acc[J * i + j] * inv);
+            }
+        }
+      }
+    } else {
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const int r = nt * 16 + n;
+        if (r < a.rows) {
+          const float inv = lrow[nt] > 0.f ? 1.f / lrow[nt] : 0.f;
+          q_t* orow = out + out_row(r);
+#pragma unroll
+          for (int j = 0; j < J; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int d = Core::out_dim(g, j, i);
+              if (d < D) orow[d] = Cvt<CT>::from_f32(ctx > 0 ? core.out_val(nt, j, i) * inv : 0.f);
+            }
+        }
+      }
+    }
+
+    if (u.g + lend >= s1) break;
+    // next unit: (b, kvh + 1) or (b + 1, 0)
+    u.g += u.n;
+    if (u.kvh + 1 < H) {
+      ++u.kvh;
+    } else {
+      ++u.b;
+      u.kvh = 0;
+      u.n = unit_steps(__builtin_amdgcn_readfirstlane(a.ctx_lens[u.b]), a.max_ctx);
+    }
+    ls = 0;
+    first_unit = false;
+  }
+}
+
+// ------------------------------------------------------------------ dispatch
+// A launcher sets a.num_waves (at most `cap`) to what the device keeps
+// resident at once, so that every wave's slice streams concurrently.
+typedef int (*DecodeFn)(DecodeArgs&, int cap, hipStream_t);
+
+static int device_cus() {
+  static int cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
+
+template <class CT, class KVT, class ST, int D, int NT, bool BIG>
+int launch_decode_kernel(DecodeArgs& a, int cap, hipStream_t s) {
+  static int groups_per_cu = 0;
+  if (!groups_per_cu) {
+    int nb = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &nb, reinterpret_cast<const void*>(&decode_kernel<CT, KVT, ST, D, NT, BIG>),
+            64 * kWavesPerGroup, 0) != hipSuccess || nb <= 0)
+      nb = 1;
+    groups_per_cu = nb;
+  }
+  const long resident = (long)device_cus() * groups_per_cu * kWavesPerGroup;
+  a.num_waves = (int)std::max(1L, std::min<long>(cap, resident));
+  const unsigned groups = (unsigned)((a.num_waves + kWavesPerGroup - 1) / kWavesPerGroup);
+  hipLaunchKernelGGL((decode_kernel<CT, KVT, ST, D, NT, BIG>), dim3(groups), dim3(64 * kWavesPerGroup),
+                     0, s, a);
+  return check_launch("hpa_paged_decode");
+}
+
+template <class CT, class KVT, class ST, int D, int NT>
+int launch_decode(DecodeArgs& a, int cap, hipStream_t s) {
+  // block_size >= 16 takes the scalar-addressed fast path
+  if (a.bs_log2 >= 4) return launch_decode_kernel<CT, KVT, ST, D, NT, true>(a, cap, s);
+  return launch_decode_kernel<CT, KVT, ST, D, NT, false>(a, cap, s);
+}
+
+template <class CT, class KVT, class ST, int D>
+DecodeFn pick_nt(int nt) {
+  switch (nt) {
+    case 1: return launch_decode<CT, KVT, ST, D, 1>;
+    case 2: return launch_decode<CT, KVT, ST, D, 2>;
+    case 4: return launch_decode<CT, KVT, ST, D, 4>;
+  }
+  return nullptr;
+}
+template <class CT, class KVT, class ST>
+DecodeFn pick_d(int d, int nt) {
+  switch (d) {
+    case 8: return pick_nt<CT, KVT, ST, 8>(nt);
+    case 16: return pick_nt<CT, KVT, ST, 16>(nt);
+    case 32: return pick_nt<CT, KVT, ST, 32>(nt);
+    case 64: return pick_nt<CT, KVT, ST, 64>(nt);
+    case 128: return pick_nt<CT, KVT, ST, 128>(nt);
+    case 256: return pick_nt<CT, KVT, ST, 256>(nt);
+  }
+  return nullptr;
+}
+
+// Kernel table of one compute type; each is instantiated in its own
+// translation unit (hpa_decode_{f32,f16,bf16}.hip) so the builds run in
+// parallel.
+template <class CT>
+DecodeFn pick_kv(int kv_dtype, int scale_dtype, int d, int nt) {
+  if (kv_dtype == HPA_I8) {
+    if (scale_dtype == HPA_F16) return pick_d<CT, I8, F16>(d, nt);
+    if (scale_dtype == HPA_F32) return pick_d<CT, I8, F32>(d, nt);
+    return nullptr;
+  }
+  if (kv_dtype != CT::code) return nullptr;
+  return pick_d<CT, CT, F32>(d, nt);
+}
+
+extern template DecodeFn pick_kv<F32>(int, int, int, int);
+extern template DecodeFn pick_kv<F16>(int, int, int, int);
+extern template DecodeFn pick_kv<BF16>(int, int, int, int);
+
+}  // namespace hpa

@@ -38,7 +38,7 @@ struct PrefillArgs {
 constexpr int kPrefillWaves = 4;
 constexpr int kPrefillNT = 2;
 
-template <class CT, class KVT, class ST, int D, int NT, int NW>
+template <class CT, class KVT, class ST, int D, int NT, int NW, bool BIG>
 __global__ __launch_bounds__(64 * NW) void prefill_kernel(const PrefillArgs a) {
   typedef AttnCore<CT, KVT, ST, D, NT> Core;
   typedef typename CT::storage q_t;
@@ -81,13 +81,15 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(const PrefillArgs a) {
 
   const typename Core::LaneOff lo = Core::lane_off();
   if (maxlim > 0) {
+    TableWindow win;
+    if (BIG) win.fill(pv.table, pv.table_stride, 0);
     int k0 = 0;
     typename Core::Raw cur;
-    Core::load_any(pv, k0, lo, cur);
+    Core::template load_sel<BIG>(pv, win, k0, lo, cur);
     for (;;) {
       const int kn = k0 + 32;
       typename Core::Raw nxt;
-      if (kn < maxlim) Core::load_any(pv, kn, lo, nxt);
+      if (kn < maxlim) Core::template load_sel<BIG>(pv, win, kn, lo, nxt);
       core.compute(cur, k0, a.scale_log2, k0 + 32 > minlim, ctx);
       if (kn >= maxlim) break;
       cur = nxt;
@@ -116,8 +118,12 @@ typedef void (*PrefillFn)(const PrefillArgs&, dim3, hipStream_t);
 
 template <class CT, class KVT, class ST, int D>
 void launch_prefill(const PrefillArgs& a, dim3 grid, hipStream_t s) {
-  hipLaunchKernelGGL((prefill_kernel<CT, KVT, ST, D, kPrefillNT, kPrefillWaves>), grid,
-                     dim3(64 * kPrefillWaves), 0, s, a);
+  if (a.bs_log2 >= 4)
+    hipLaunchKernelGGL((prefill_kernel<CT, KVT, ST, D, kPrefillNT, kPrefillWaves, true>), grid,
+                       dim3(64 * kPrefillWaves), 0, s, a);
+  else
+    hipLaunchKernelGGL((prefill_kernel<CT, KVT, ST, D, kPrefillNT, kPrefillWaves, false>), grid,
+                       dim3(64 * kPrefillWaves), 0, s, a);
 }
 template <class CT, class KVT, class ST>
 PrefillFn pick_pd(int d) {

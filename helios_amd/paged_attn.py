@@ -397,7 +397,7 @@ def paged_attention_decode_hip(
             raise ValueError(f"workspace holds {workspace.nbytes} bytes, {ws_bytes} needed")
         ws = workspace
     else:
-        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
+        ws = _cached_workspace(dev, ws_bytes)
     quant = k_cache.dtype == torch.int8
     st = L.hpa_paged_decode(
         ptr(query), ptr(out), DTYPE_CODE[query.dtype], ptr(k_cache), ptr(v_cache),
@@ -410,6 +410,23 @@ def paged_attention_decode_hip(
     )
     check(st, "hpa_paged_decode")
     return out
+
+
+_WORKSPACES: dict = {}
+
+
+def _cached_workspace(device: torch.device, nbytes: int) -> Optional[torch.Tensor]:
+    """The decode kernel's split-K workspace, one per device, grown on demand.
+    It starts zero-filled and every call leaves its arrival counters at zero,
+    so calls ordered on one stream can share it."""
+    if nbytes == 0:
+        return None
+    key = (device.type, device.index if device.index is not None else torch.cuda.current_device())
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = ws
+    return ws
 
 
 def decode_workspace_bytes(n_seqs: int, q_per_seq: int, n_q_heads: int, n_kv_heads: int,

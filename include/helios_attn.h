@@ -77,8 +77,14 @@ size_t hpa_decode_workspace_size(int num_seqs, int q_per_seq, int num_q_heads, i
  * (helios' causal rule, paged_attn.py:401-404, with start_pos = context -
  * q_per_seq).  An empty context yields zeros.  Softmax scale sm_scale.
  * The query rows of one KV head ((num_q_heads / num_kv_heads) * q_per_seq)
- * must not exceed 64; use hpa_paged_prefill beyond that.  workspace: at least
- * hpa_decode_workspace_size(...) bytes of device memory (may be NULL if 0). */
+ * must not exceed 64; use hpa_paged_prefill beyond that.
+ * part_tokens: smallest share of the context, in tokens, one wave streams
+ * (0 = library default); it changes only the summation order.
+ * workspace: at least hpa_decode_workspace_size(...) bytes of device memory
+ * (may be NULL if that is 0), zero-filled before its first use.  It holds
+ * per-(sequence, KV head) arrival counters that every completed call leaves
+ * at zero again, so one workspace serves any number of calls ordered on one
+ * stream; calls that may run concurrently need separate workspaces. */
 int hpa_paged_decode(const void* q, void* out, int q_dtype, const void* k_pool, const void* v_pool,
                      int kv_dtype, const void* k_scale, const void* v_scale, int scale_dtype,
                      const int32_t* block_tables, int table_stride, const int32_t* context_lens,

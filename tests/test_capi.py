@@ -54,12 +54,26 @@ def test_status_codes_match_header():
         assert int(m.group(1)) == getattr(_lib, name), name
 
 
+def _ws(waves, rows, D, units):
+    # a fixed 1 MiB region of int32 arrival counters (2^18 sequence x KV-head
+    # units), then per wave two partial slots of rows x (m, l) and rows x D
+    # floats
+    if waves <= 1:
+        return 0
+    assert units <= 1 << 18
+    return (1 << 20) + waves * (2 * rows * 2 * 4 + 2 * rows * D * 4)
+
+
 def test_workspace_size(lib):
-    # one partition per sequence -> no workspace
-    assert lib.hpa_decode_workspace_size(64, 1, 14, 2, 64, 256, 256) == 0
-    # split: seqs * Hkv * parts * rows * (D + 2) floats
-    got = lib.hpa_decode_workspace_size(4, 3, 32, 8, 128, 2048, 512)
-    assert got == 4 * 8 * 4 * 12 * 130 * 4
+    # one KV head, 256-token contexts, 256-token slice floor: a single wave,
+    # every unit whole, no workspace
+    assert lib.hpa_decode_workspace_size(1, 1, 4, 1, 64, 256, 256) == 0
+    # two units of 8 steps over 8-step slices: two waves, rows = 14 / 2
+    assert lib.hpa_decode_workspace_size(1, 1, 14, 2, 64, 256, 256) == _ws(2, 7, 64, 2)
+    # config 5 at the largest context: the 4096-wave cap, rows = 4 x 3
+    assert lib.hpa_decode_workspace_size(256, 3, 32, 8, 128, 32768, 0) == _ws(4096, 12, 128, 2048)
+    # a smaller slice floor never lowers the count below the cap's reach
+    assert lib.hpa_decode_workspace_size(64, 1, 14, 2, 64, 4096, 32) == _ws(4096, 7, 64, 128)
 
 
 def test_argument_errors_return_status_without_a_gpu(lib):

@@ -227,3 +227,25 @@ def test_device_tensor_tables_match_list_tables():
     a = paged_attention_decode_hip(q, cache.k_cache, cache.v_cache, tables, lens)
     b = paged_attention_decode_hip(q, cache.k_cache, cache.v_cache, tt, lt, max_context_len=700)
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("quant", [False, True])
+def test_stream_k_many_pieces_and_empty_units(quant):
+    """A 32-token slice floor cuts the long units into hundreds of pieces
+    (more than the merge keeps in LDS) and puts empty contexts between cut
+    units; empty contexts give zeros, the rest match the oracle."""
+    lens = [0, 5000, 0, 1, 33, 2049, 0]
+    cache, tables, q = _case(90, len(lens), lens, 8, 2, 64, 16, torch.float16, quant=quant)
+    ks = cache.k_scale if quant else None
+    vs = cache.v_scale if quant else None
+    got = paged_attention_decode_hip(q, cache.k_cache, cache.v_cache, tables, lens,
+                                     k_scale=ks, v_scale=vs, part_tokens=32)
+    live = [i for i, c in enumerate(lens) if c > 0]
+    want = _oracle_decode(cache, q[live], [tables[i] for i in live], [lens[i] for i in live])
+    _check(got[live], want, torch.float16, "stream-K pieces")
+    dead = [i for i, c in enumerate(lens) if c == 0]
+    assert torch.count_nonzero(got[dead]) == 0
+    # the slice floor only reorders the summation
+    other = paged_attention_decode_hip(q, cache.k_cache, cache.v_cache, tables, lens,
+                                       k_scale=ks, v_scale=vs)
+    assert max_abs(to_np(got), to_np(other)) <= 2e-3
