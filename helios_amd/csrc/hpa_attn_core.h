@@ -92,6 +92,16 @@ struct TableWindow {
     w1 = b0 + 64 + lane < stride ? (uint32_t)row[b0 + 64 + lane] : 0u;
   }
 
+  // Fill and wait for it here, so that later reads of the window never make
+  // the compiler wait for loads that are still in flight (a KV prefetch
+  // issued after a possible refill would otherwise be drained at every read).
+  __device__ __forceinline__ void fill_sync(const int32_t* row, int stride, int b0) {
+    fill(row, stride, b0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  }
+
   __device__ __forceinline__ int get(int lb) const {
     const int i = lb - base;
     return i < 64 ? __builtin_amdgcn_readlane((int)w0, i) : __builtin_amdgcn_readlane((int)w1, i - 64);
@@ -331,30 +341,46 @@ struct AttnCore {
   }
 
   // Both tiles of the 32-key step starting at k0 (wave-uniform), fast path.
-  __device__ __forceinline__ static void load_big(const PoolView& pv, TableWindow& win, int k0,
-                                                  const LaneOff& lo, Raw& r) {
+  // With `enable` false every tile is a zero-length resource: the load
+  // instructions still issue (so the compiler's wait counts do not depend on
+  // a branch) but return zeros without touching memory.
+  __device__ __forceinline__ static void load_big(const PoolView& pv, const TableWindow& win, int k0,
+                                                  const LaneOff& lo, Raw& r, bool enable = true) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       const int key0 = k0 + 16 * t;
-      const bool valid = key0 < pv.ctx;
+      const bool valid = enable && key0 < pv.ctx;
       int phys = 0;
       if (valid) {
-        const int lb = key0 >> pv.bs_log2;
-        if (!win.covers(lb)) win.fill(pv.table, pv.table_stride, lb);
-        phys = win.get(lb);
+        // the caller keeps the window covering every valid tile it loads
+        phys = win.get(key0 >> pv.bs_log2);
         phys = (unsigned)phys < (unsigned)pv.num_blocks ? phys : 0;  // never leave the pool
       }
       load_tile(pv, t, key0, phys, valid, lo, r);
     }
   }
 
+  // Makes `win` cover the blocks of the 32-key step at k0 (fast path only);
+  // a refill waits for its load.
+  template <bool BIG>
+  __device__ __forceinline__ static void cover(const PoolView& pv, TableWindow& win, int k0) {
+    if constexpr (BIG) {
+      const int last = min(k0 + 31, pv.ctx - 1);
+      if (last >= k0 && !(win.covers(k0 >> pv.bs_log2) && win.covers(last >> pv.bs_log2)))
+        win.fill_sync(pv.table, pv.table_stride, k0 >> pv.bs_log2);
+    }
+  }
+
+  // One step's loads.  Fast path: issued unconditionally, `enable` false
+  // makes them empty; general path: nothing is issued when disabled.
   template <bool BIG>
   __device__ __forceinline__ static void load_sel(const PoolView& pv, TableWindow& win, int k0,
-                                                  const LaneOff& lo, Raw& r) {
+                                                  const LaneOff& lo, Raw& r, bool enable = true) {
     if constexpr (BIG) {
-      load_big(pv, win, k0, lo, r);
+      if (enable) cover<BIG>(pv, win, k0);
+      load_big(pv, win, k0, lo, r, enable);
     } else {
-      load(pv, k0, r);
+      if (enable) load(pv, k0, r);
     }
   }
 

@@ -25,7 +25,7 @@ static DecodePlan plan_decode(int num_seqs, int num_kv_heads, int max_context_le
   DecodePlan p;
   const int mt = min_tokens > 0 ? std::min(min_tokens, 1 << 20) : kDefaultMinTokens;
   p.min_steps = std::max(1, (mt + 31) / 32);
-  const long per_unit = std::max(1, (max_context_len + 31) / 32);
+  const long per_unit = std::max(1, (max_context_len + 31) / 32) + kUnitCost;
   const long ub = (long)num_seqs * num_kv_heads * per_unit;
   const long w = (ub + p.min_steps - 1) / p.min_steps;
   p.waves = (int)std::max(1L, std::min<long>(w, kWaveCap));

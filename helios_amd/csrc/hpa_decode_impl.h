@@ -60,7 +60,17 @@ struct DecodeArgs {
 
 constexpr int kWavesPerGroup = 4;
 constexpr int kWaveCap = 4096;          // 256 CUs x 16 resident waves
+// Steps of KV loads in flight per wave.  The kernel runs one wave per SIMD:
+// two waves sharing a SIMD are served oldest-first, so with equal slices the
+// younger one finishes long after the older, while a single wave with a deep
+// pipeline keeps the SIMD's share of HBM busy on its own.
+constexpr int kDepth = 3;
 constexpr int kDefaultMinTokens = 256;  // per-wave slice floor (8 steps)
+// What a unit costs beyond its steps, in step-equivalents: its prologue
+// (table window, query rows, first loads in flight) and epilogue (output or
+// partial stores, arrival count, possibly the merge).  Slices are cut on
+// steps plus this, so waves holding many short units get fewer steps.
+constexpr int kUnitCost = 4;
 
 __device__ __forceinline__ int unit_steps(int ctx, int max_ctx) {
   ctx = min(ctx, max_ctx);
@@ -87,10 +97,11 @@ __device__ __forceinline__ int wave_incl_scan_i(int x) {
 struct UnitPos {
   int b, kvh;  // unit
   int n;       // its steps
-  int g;       // global index of its first step
+  int g;       // global position where its cost range starts
 };
 
-// Steps per KV head summed over all sequences (identical in every wave).
+// Cost (steps + kUnitCost per unit) per KV head summed over all sequences
+// (identical in every wave).
 __device__ int total_steps_per_head(const DecodeArgs& a) {
   const int lane = threadIdx.x & 63;
   int acc = 0;
@@ -103,12 +114,14 @@ __device__ int total_steps_per_head(const DecodeArgs& a) {
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      if (base + 64 * i + lane < a.num_seqs) acc += unit_steps(c[i], a.max_ctx);
+      if (base + 64 * i + lane < a.num_seqs) acc += unit_steps(c[i], a.max_ctx) + kUnitCost;
   }
   return wave_sum_i(acc);
 }
 
-// The unit holding global step s0 (< total).  Wave-uniform result.
+// The unit whose cost range holds global position s0 (< total).  A unit's
+// range is kUnitCost positions of overhead followed by its steps.
+// Wave-uniform result.
 __device__ UnitPos locate(const DecodeArgs& a, int s0) {
   const int lane = threadIdx.x & 63;
   const int H = a.num_kv_heads;
@@ -117,8 +130,9 @@ __device__ UnitPos locate(const DecodeArgs& a, int s0) {
   for (int base = 0; base < a.num_seqs; base += 64) {
     const int b = base + lane;
     const int n = b < a.num_seqs ? unit_steps(a.ctx_lens[b], a.max_ctx) : 0;
-    const int incl = wave_incl_scan_i(n);
-    const int first = H * (run + incl - n);  // global first step of sequence b
+    const int c = b < a.num_seqs ? n + kUnitCost : 0;
+    const int incl = wave_incl_scan_i(c);
+    const int first = H * (run + incl - c);  // global first position of sequence b
     const int last = H * (run + incl);       // one past its last
     const unsigned long long hit =
         __builtin_amdgcn_ballot_w64(b < a.num_seqs && first <= s0 && s0 < last);
@@ -128,8 +142,8 @@ __device__ UnitPos locate(const DecodeArgs& a, int s0) {
       const int nb = __builtin_amdgcn_readfirstlane(__shfl(n, l));
       p.b = base + l;
       p.n = nb;
-      p.kvh = (s0 - fb) / nb;
-      p.g = fb + p.kvh * nb;
+      p.kvh = (s0 - fb) / (nb + kUnitCost);
+      p.g = fb + p.kvh * (nb + kUnitCost);
       return p;
     }
     run += __builtin_amdgcn_readfirstlane(__shfl(incl, 63));
@@ -169,17 +183,19 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
   UnitPos u = locate(a, s0);
 
   const typename Core::LaneOff lo = Core::lane_off();
-  int ls = s0 - u.g;  // local step inside the unit
+  int ls = max(s0 - (u.g + kUnitCost), 0);  // first local step of the unit in the slice
   bool first_unit = true;
 
   for (;;) {
     const int ctx = min(__builtin_amdgcn_readfirstlane(a.ctx_lens[u.b]), a.max_ctx);
+    const int sb = u.g + kUnitCost;  // global position of the unit's step 0
     const int lbeg = ls;
-    const int lend = min(u.n, ls + (s1 - (u.g + ls)));  // steps of this unit in the slice
+    const int lend = min(u.n, s1 - sb);  // steps of this unit in the slice: [lbeg, lend)
+    if (lend <= lbeg) break;  // the slice ends inside the unit's overhead: the next wave has it
     const PoolView pv{a.k, a.v, a.ks, a.vs, a.tables + (long)u.b * a.table_stride, a.table_stride,
                       u.kvh, H, a.bs_log2, a.num_blocks, ctx};
     TableWindow win;
-    if (BIG && ctx > 0) win.fill(pv.table, pv.table_stride, (32 * lbeg) >> a.bs_log2);
+    if (BIG && ctx > 0) win.fill(pv.table, pv.table_stride, (32 * lbeg) >> a.bs_log2);  // waited on at first use
 
     // ---- unit prologue: query rows of (u.b, u.kvh)
     auto out_row = [&](int r) -> long {
@@ -205,15 +221,27 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
 
     // ---- stream the unit's steps [lbeg, lend) with one step in flight
     if (ctx > 0) {
-      typename Core::Raw cur;
-      Core::template load_sel<BIG>(pv, win, 32 * lbeg, lo, cur);
-      for (int st = lbeg;; ++st) {
-        typename Core::Raw nxt;
-        const bool last = st + 1 >= lend;
-        if (!last) Core::template load_sel<BIG>(pv, win, 32 * (st + 1), lo, nxt);
-        core.compute(cur, 32 * st, a.scale_log2, 32 * st + 32 > minlim, ctx);
-        if (last) break;
-        cur = nxt;
+      // A ring of kDepth + 1 register buffers, unrolled so every index is a
+      // compile-time constant: kDepth steps of loads stay in flight while a
+      // step computes, and no buffer is ever copied (a register copy of data
+      // still in flight would make the compiler wait for it).
+      constexpr int NB = kDepth + 1;
+      typename Core::Raw rb[NB];
+#pragma unroll
+      for (int k = 0; k < kDepth; ++k)
+        Core::template load_sel<BIG>(pv, win, 32 * (lbeg + k), lo, rb[k], lbeg + k < lend);
+      bool done = false;
+      for (int st = lbeg; !done; st += NB) {
+#pragma unroll
+        for (int k = 0; k < NB; ++k) {
+          if (!done) {
+            const int cur = st + k;
+            Core::template load_sel<BIG>(pv, win, 32 * (cur + kDepth), lo, rb[(k + kDepth) % NB],
+                                         cur + kDepth < lend);
+            core.compute(rb[k], 32 * cur, a.scale_log2, 32 * cur + 32 > minlim, ctx);
+            done = cur + 1 >= lend;
+          }
+        }
       }
     }
 
@@ -250,7 +278,7 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
                 (uint32_t)((slot * a.rows + r) * 8), 0, kCoherent);
         }
       }
-      const int wa = u.g / per, wb = (u.g + u.n - 1) / per;  // waves holding the pieces
+      const int wa = sb / per, wb = (sb + u.n - 1) / per;  // waves holding the pieces
       const int unit = u.b * H + u.kvh;
       // the piece's stores are complete (hence visible device-wide) before
       // the counter moves
@@ -265,7 +293,8 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
         // the workspace (this wave's own included), so every merging wave
         // evaluates the same expression
         if (lane == 0) __hip_atomic_store(a.counters + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const long slot_a = 2L * wa + (wa * per == u.g ? 0 : 1);
+        // wave wa saw this unit first iff its slice began inside the unit's range
+        const long slot_a = 2L * wa + (wa * per >= u.g ? 0 : 1);
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
           const int r = nt * 16 + n;
@@ -334,9 +363,9 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
       }
     }
 
-    if (u.g + lend >= s1) break;
+    if (sb + lend >= s1) break;
     // next unit: (b, kvh + 1) or (b + 1, 0)
-    u.g += u.n;
+    u.g += u.n + kUnitCost;
     if (u.kvh + 1 < H) {
       ++u.kvh;
     } else {

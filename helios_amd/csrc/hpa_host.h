@@ -5,7 +5,7 @@
 #include <stdarg.h>
 #include <stdint.h>
 
-#include "../../include/helios_attn.h"
+#include "helios_attn.h"
 
 namespace hpa {
 

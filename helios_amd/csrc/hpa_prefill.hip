@@ -89,7 +89,7 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(const PrefillArgs a) {
     for (;;) {
       const int kn = k0 + 32;
       typename Core::Raw nxt;
-      if (kn < maxlim) Core::template load_sel<BIG>(pv, win, kn, lo, nxt);
+      Core::template load_sel<BIG>(pv, win, kn, lo, nxt, kn < maxlim);
       core.compute(cur, k0, a.scale_log2, k0 + 32 > minlim, ctx);
       if (kn >= maxlim) break;
       cur = nxt;

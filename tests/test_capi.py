@@ -64,15 +64,23 @@ def _ws(waves, rows, D, units):
     return (1 << 20) + waves * (2 * rows * 2 * 4 + 2 * rows * D * 4)
 
 
+def _waves(seqs, kv_heads, max_ctx, part_tokens):
+    # host bound on the work, in 32-key steps plus 4 per (sequence, KV head)
+    # unit, cut into slices of at least part_tokens / 32 steps, capped at 4096
+    min_steps = max(1, ((part_tokens or 256) + 31) // 32)
+    ub = seqs * kv_heads * (max(1, (max_ctx + 31) // 32) + 4)
+    return max(1, min((ub + min_steps - 1) // min_steps, 4096))
+
+
 def test_workspace_size(lib):
-    # one KV head, 256-token contexts, 256-token slice floor: a single wave,
-    # every unit whole, no workspace
-    assert lib.hpa_decode_workspace_size(1, 1, 4, 1, 64, 256, 256) == 0
-    # two units of 8 steps over 8-step slices: two waves, rows = 14 / 2
-    assert lib.hpa_decode_workspace_size(1, 1, 14, 2, 64, 256, 256) == _ws(2, 7, 64, 2)
+    # one unit that fits one slice: a single wave, every unit whole, no workspace
+    assert _waves(1, 1, 32, 256) == 1
+    assert lib.hpa_decode_workspace_size(1, 1, 4, 1, 64, 32, 256) == 0
+    # two units of 8 steps (+4 each) over 8-step slices: rows = 14 / 2
+    assert lib.hpa_decode_workspace_size(1, 1, 14, 2, 64, 256, 256) == _ws(_waves(1, 2, 256, 256), 7, 64, 2)
     # config 5 at the largest context: the 4096-wave cap, rows = 4 x 3
+    assert _waves(256, 8, 32768, 0) == 4096
     assert lib.hpa_decode_workspace_size(256, 3, 32, 8, 128, 32768, 0) == _ws(4096, 12, 128, 2048)
-    # a smaller slice floor never lowers the count below the cap's reach
     assert lib.hpa_decode_workspace_size(64, 1, 14, 2, 64, 4096, 32) == _ws(4096, 7, 64, 128)
 
 
