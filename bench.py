@@ -329,11 +329,27 @@ def main():
                     help="pool copies rotated per step (default: enough to exceed 256 MB)")
     ap.add_argument("--cpu-budget", type=float, default=15.0,
                     help="seconds of CPU baseline work (0 disables it)")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only run 5 plain device copies of MIB MiB (the known-size kernel "
+                         "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings) and exit")
     args = ap.parse_args()
+
+    if args.calibrate_copy:
+        import torch
+
+        n = args.calibrate_copy << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes": n, "copies": 5}))
+        return
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this build runs on one GPU only: the paged-attention path "
-                                   "has no multi-GPU mode (see DESIGN.md, sharding)",
+                                   "has no multi-GPU mode (sequences and KV heads shard "
+                                   "without exchange; one GPU's share is what is measured)",
                           "n_gpus": args.gpus}))
         sys.exit(2)
 
