@@ -257,6 +257,7 @@ class PrefillWorkload(Workload):
             t.normal_(generator=gen)
         self.q = torch.randn(B * T, Hq, D, generator=gen, device=device, dtype=torch.float16)
         self.qlens = torch.full((B,), T, dtype=torch.int32, device=device)
+        self.cu = torch.arange(0, (B + 1) * T, T, dtype=torch.int32, device=device)
         self.pos_t = torch.tensor(priors, dtype=torch.int32, device=device)
         self.ctx_t = torch.tensor(ctxs, dtype=torch.int32, device=device)
         self.scale = 1.0 / math.sqrt(D)
@@ -269,7 +270,8 @@ class PrefillWorkload(Workload):
         import helios_amd as H
 
         H.paged_attention_varlen(self.q, self.cache, self.tables_t, self.qlens, self.pos_t,
-                                 self.ctx_t, self.scale, max_query_len=self.T)
+                                 self.ctx_t, self.scale, max_query_len=self.T,
+                                 cu_query_lens=self.cu)
 
     def config(self):
         return {"workload": self.name, "sequences": self.B, "chunk": self.T,

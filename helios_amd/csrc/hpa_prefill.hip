@@ -15,25 +15,11 @@
 // that cross the causal diagonal pay for element-wise masking.
 #include "hpa_attn_core.h"
 #include "hpa_host.h"
+#include "hpa_prefill.h"
 
 namespace hpa {
 
-struct PrefillArgs {
-  const void* q;
-  void* out;
-  const void* k;
-  const void* v;
-  const void* ks;
-  const void* vs;
-  const int32_t* tables;
-  int table_stride;
-  const int32_t* cu_q;
-  const int32_t* q_pos;
-  const int32_t* ctx_lens;
-  int num_seqs, num_q_heads, num_kv_heads, group;
-  int bs_log2, num_blocks;
-  float scale_log2;
-};
+
 
 constexpr int kPrefillWaves = 4;
 constexpr int kPrefillNT = 2;
@@ -206,6 +192,8 @@ extern "C" int hpa_paged_prefill(const void* q, void* out, int q_dtype, const vo
   a.bs_log2 = bsl;
   a.num_blocks = num_blocks;
   a.scale_log2 = sm_scale * 1.4426950408889634f;
+  if (launch_prefill_mfma(a, q_dtype, kv_dtype, head_dim, max_q_len, stream))
+    return check_launch("hpa_paged_prefill");
   const long rows = (long)max_q_len * a.group;
   const long per_wg = (long)kPrefillWaves * kPrefillNT * 16;
   dim3 grid((unsigned)((rows + per_wg - 1) / per_wg), (unsigned)num_kv_heads, (unsigned)num_seqs);

@@ -523,13 +523,17 @@ def paged_attention_varlen(
     context_lens: LensArg,
     scale: Optional[float] = None,
     max_query_len: Optional[int] = None,
+    cu_query_lens: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Causal attention for a ragged batch of prompt chunks in one launch.
 
     query [sum(query_lens), n_q_heads, head_dim]; sequence b's token i sits at
     start_positions[b] + i and attends keys [0, min(start + i + 1,
     context_lens[b])).  Row-for-row equal to calling paged_attention_prefill
-    per sequence, which is what reference exec/model.py:303-317 does."""
+    per sequence, which is what reference exec/model.py:303-317 does.
+    ``cu_query_lens`` (int32 device tensor [n + 1], the prefix sums of
+    ``query_lens``) and ``max_query_len`` may be passed to skip building them
+    per call."""
     _require_gpu(query, "query")
     n_tok, n_q_heads, head_dim = query.shape
     scale = scale or 1.0 / math.sqrt(head_dim)
@@ -541,7 +545,12 @@ def paged_attention_varlen(
         for blocks, ctx in zip(block_tables, (context_lens.tolist() if isinstance(context_lens, torch.Tensor) else context_lens)):
             _check_context(blocks, int(ctx), kv_cache.block_size, kv_cache.num_blocks)
         tables = _padded_tables(block_tables, dev)
-    if isinstance(query_lens, torch.Tensor):
+    if cu_query_lens is not None:
+        cu = cu_query_lens
+        n_seqs = cu.numel() - 1
+        if max_query_len is None:
+            max_query_len = int((cu[1:] - cu[:-1]).max().item()) if n_seqs > 0 else 0
+    elif isinstance(query_lens, torch.Tensor):
         qlens_t = query_lens.to(device=dev, dtype=torch.int32)
         cu = torch.zeros(qlens_t.numel() + 1, dtype=torch.int32, device=dev)
         cu[1:] = torch.cumsum(qlens_t, 0)
