@@ -33,9 +33,9 @@
 // the V reads (one key x all chunks) hit distinct banks.
 #include <type_traits>
 
+#include "hpa_attn_core.h"
 #include "hpa_host.h"
 #include "hpa_prefill.h"
-#include "hpa_types.h"
 
 namespace hpa {
 
@@ -96,6 +96,7 @@ __global__ __launch_bounds__(64 * kPfWaves, 2) void prefill_mfma_kernel(const Pr
   constexpr int VW = (DB * 2 + 3) / 4;  // u32 words of V per key per lane
   constexpr int IPW = NCH / 4;        // global->LDS instructions per wave per step
   static_assert(D == 64 || D == 128, "head_dim 64 or 128");
+  static_assert(kPfStages == 3, "the step loop is unrolled by three");
   __shared__ __attribute__((aligned(16))) uint8_t smem[kPfStages][2 * TILEB];
 
   // heaviest (last) row tiles first; the units of one tile index spread over
@@ -137,40 +138,64 @@ __global__ __launch_bounds__(64 * kPfWaves, 2) void prefill_mfma_kernel(const Pr
       qf[c] = rv ? *reinterpret_cast<const u32x4*>(qrow + 8 * c) : (u32x4){0, 0, 0, 0};
   }
 
-  // ---- cooperative global->LDS copy of one step's K and V tiles
-  const int32_t* trow = tables + (long)b * a.table_stride;
+  // ---- cooperative global->LDS copy.  Wave w copies tensor w / 2 (K, V),
+  // 16-key half w % 2 of every step: IPW instructions of 64 lanes x 16 bytes.
+  // Lane offsets (global side, swizzle applied) are the same every step.
+  const int tensor = w >> 1, half = w & 1;
+  uint32_t voff[IPW];
+#pragma unroll
+  for (int i = 0; i < IPW; ++i) {
+    const int P = (w * IPW + i) * 64 + lane;     // chunk position in [K tile | V tile]
+    const int row = (P % (32 * NCH)) / NCH, q = P % NCH;
+    voff[i] = (uint32_t)((row & 15) * ROWB + (q ^ (row % NCH)) * 16);
+  }
+  const char* pool = reinterpret_cast<const char*>(tensor ? a.v : a.k);
+  const long blk_rows = (long)a.num_kv_heads << a.bs_log2;   // key rows per block
+  const long head_rows = (long)kvh << a.bs_log2;
   const int bsm = (1 << a.bs_log2) - 1;
-  const long head_slab = (long)kvh << a.bs_log2;  // in key rows, within a block
+  const int32_t* trow = tables + (long)b * a.table_stride;
+  TableWindow win;
+  if (nsteps > 0) win.fill(trow, a.table_stride, 0);
   auto issue_loads = [&](int step, int stage) {
-    const int k0 = step * 32;
+    const int key0 = step * 32 + 16 * half;
+    int valid = min(max(ctx - key0, 0), 16);     // rows past the context read as zeros
+    int phys = 0;
+    if (valid > 0) {
+      const int lb = key0 >> a.bs_log2;
+      if (!win.covers(lb)) win.fill_sync(trow, a.table_stride, lb);
+      phys = win.get(lb);
+      if ((unsigned)phys >= (unsigned)a.num_blocks) { phys = 0; valid = 0; }
+    }
+    const char* base = pool + ((long)phys * blk_rows + head_rows + (key0 & bsm)) * ROWB;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), (short)0, valid * ROWB, 0x00020000);
 #pragma unroll
     for (int i = 0; i < IPW; ++i) {
-      const int I = w * IPW + i;                  // instruction index within the workgroup
-      const int P0 = I * 64;                      // first chunk position it fills
-      const int tensor = P0 / (32 * NCH);         // 0 = K, 1 = V
-      const int prow0 = (P0 % (32 * NCH)) / NCH;  // first key row it fills
-      const int half = prow0 >> 4;                // 16-key half of the tile
-      const int key0 = k0 + 16 * half;
-      int valid = min(max(ctx - key0, 0), 16);    // rows past the context read as zeros
-      int phys = 0;
-      if (valid > 0) {
-        int lb = key0 >> a.bs_log2;
-        lb = lb < a.table_stride ? lb : a.table_stride - 1;
-        phys = trow[lb];
-        if ((unsigned)phys >= (unsigned)a.num_blocks) { phys = 0; valid = 0; }
-      }
-      const long slot0 = (long)phys * ((long)a.num_kv_heads << a.bs_log2) + head_slab + (key0 & bsm);
-      const char* base = reinterpret_cast<const char*>(tensor ? a.v : a.k) + slot0 * ROWB;
-      const __amdgpu_buffer_rsrc_t rs =
-          __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), (short)0, valid * ROWB, 0x00020000);
-      const int P = P0 + lane;
-      const int row = (P % (32 * NCH)) / NCH, q = P % NCH;
-      const int j = q ^ (row % NCH);              // global chunk that lands at position q
-      const uint32_t voff = (uint32_t)((row & 15) * ROWB + j * 16);
+      // a local copy: the host pass of this builtin rejects a captured array
+      // element, which would silently drop the kernel's launch stub
+      const int vo = (int)voff[i];
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rs, (__attribute__((address_space(3))) void*)(&smem[stage][0] + P0 * 16), 16, voff, 0, 0, 0);
+          rs, (__attribute__((address_space(3))) void*)(&smem[stage][0] + (w * IPW + i) * 64 * 16), 16, vo, 0, 0, 0);
     }
   };
+
+  // ---- per-lane LDS offsets of the operand reads (same in every stage)
+  uint32_t koff[KCH], vofs[2][8];
+#pragma unroll
+  for (int c = 0; c < KCH; ++c) {
+    const int jj = h * (NCH / 2) + c;
+    koff[c] = (uint32_t)((n * NCH + (jj ^ (n % NCH))) * 16);
+  }
+  {
+    const int jv = (DB * 2 * n) / 16, off = (DB * 2 * n) % 16;
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+      for (int s2 = 0; s2 < 8; ++s2) {
+        const int key = 8 * (2 * kc + (s2 >> 2)) + 4 * h + (s2 & 3);
+        vofs[kc][s2] = (uint32_t)(TILEB + (key * NCH + (jv ^ (key % NCH))) * 16 + off);
+      }
+  }
 
   f32x16 o[DB];
 #pragma unroll
@@ -178,62 +203,61 @@ __global__ __launch_bounds__(64 * kPfWaves, 2) void prefill_mfma_kernel(const Pr
   float m = -INFINITY, l = 0.f;
   const float cs = a.scale_log2;
 
-  if (nsteps > 0) issue_loads(0, 0);
-  if (nsteps > 1) issue_loads(1, 1);
-  for (int i = 0; i < nsteps; ++i) {
-    const int stage = i % kPfStages;
-    // this wave's copies for step i have landed (those for i + 1 may still fly)
+  // one step: wait for its copies, barrier, issue the copies two steps ahead,
+  // then compute (STAGE folds to a constant in every unrolled call)
+  auto step = [&](int i, const int STAGE) {
     if (i + 1 < nsteps) {
-      __builtin_amdgcn_s_waitcnt(0x0F70 | IPW);  // vmcnt(IPW)
+      __builtin_amdgcn_s_waitcnt(0x0F70 | IPW);  // vmcnt(IPW): this wave's copies for step i landed
     } else {
       __builtin_amdgcn_s_waitcnt(0x0F70);        // vmcnt(0)
     }
-    __syncthreads();  // every wave's copies for step i are visible; nobody reads stage (i+2)%3 any more
-    if (i + 2 < nsteps) issue_loads(i + 2, (i + 2) % kPfStages);
+    // After the barrier every wave's copies for step i are in LDS (each
+    // waited for its own above) and every wave has consumed its reads of
+    // the stage step i + 2 refills (step i - 1).  No memory fence: a
+    // workgroup fence would also wait for the copies of step i + 1 still in
+    // flight; the signal fences keep the compiler from moving LDS accesses.
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    if (i + 2 < nsteps) issue_loads(i + 2, (STAGE + 2) % kPfStages);
     const int k0 = 32 * i;
-    if (k0 >= wave_maxlim) continue;
+    if (k0 >= wave_maxlim) return;
+    const uint8_t* st_base = &smem[STAGE][0];
 
-    const uint8_t* kt = &smem[stage][0];
-    const uint8_t* vt = &smem[stage][TILEB];
     // ---- S^T = K . Q^T
     f32x16 st = (f32x16){};
 #pragma unroll
-    for (int c = 0; c < KCH; ++c) {
-      const int jj = h * (NCH / 2) + c;
-      const u32x4 kf = *reinterpret_cast<const u32x4*>(kt + (n * NCH + (jj ^ (n % NCH))) * 16);
-      st = M::mma(kf, qf[c], st);
-    }
+    for (int c = 0; c < KCH; ++c) st = M::mma(*reinterpret_cast<const u32x4*>(st_base + koff[c]), qf[c], st);
     // ---- V rows of this lane's 16 keys, dims [DB*n, DB*n + DB)
     uint32_t vr[2][8][VW];
-    {
-      const int jv = (DB * 2 * n) / 16, off = (DB * 2 * n) % 16;
 #pragma unroll
-      for (int kc = 0; kc < 2; ++kc)
+    for (int kc = 0; kc < 2; ++kc)
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
-          const int key = 8 * (2 * kc + (s >> 2)) + 4 * h + (s & 3);
-          const uint8_t* p = vt + (key * NCH + (jv ^ (key % NCH))) * 16 + off;
-          if constexpr (VW == 2) {
-            const u32x2 x = *reinterpret_cast<const u32x2*>(p);
-            vr[kc][s][0] = x[0];
-            vr[kc][s][VW - 1] = x[1];
-          } else {
-            vr[kc][s][0] = *reinterpret_cast<const uint32_t*>(p);
-          }
+      for (int s2 = 0; s2 < 8; ++s2) {
+        const uint8_t* p = st_base + vofs[kc][s2];
+        if constexpr (VW == 2) {
+          const u32x2 x = *reinterpret_cast<const u32x2*>(p);
+          vr[kc][s2][0] = x[0];
+          vr[kc][s2][VW - 1] = x[1];
+        } else {
+          vr[kc][s2][0] = *reinterpret_cast<const uint32_t*>(p);
         }
-    }
-    // ---- online softmax over the row's 32 keys (16 here, 16 in lane ^ 32)
-    const bool masked = k0 + 32 > wave_minlim;
+      }
+    // ---- online softmax over the row's 32 keys (16 here, 16 in lane ^ 32);
+    // only steps crossing some row's limit pay for the mask
     float x[16];
+#pragma unroll
+    for (int v = 0; v < 16; ++v) x[v] = st[v];
+    if (__builtin_expect(k0 + 32 > wave_minlim, 0)) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int key = k0 + 8 * (v >> 2) + 4 * h + (v & 3);
+        x[v] = key < lim ? x[v] : -INFINITY;
+      }
+    }
     float mx = -INFINITY;
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int key = k0 + 8 * (v >> 2) + 4 * h + (v & 3);
-      float sv = st[v];
-      if (masked) sv = key < lim ? sv : -INFINITY;
-      x[v] = sv;
-      mx = fmaxf(mx, sv);
-    }
+    for (int v = 0; v < 16; ++v) mx = fmaxf(mx, x[v]);
     mx = pair_max(mx) * cs;  // scale_log2 > 0 keeps the order
     const bool grow = mx > m + (float)kPfLazy;
     if (__builtin_amdgcn_ballot_w64(grow)) {
@@ -280,6 +304,19 @@ __global__ __launch_bounds__(64 * kPfWaves, 2) void prefill_mfma_kernel(const Pr
         if constexpr (std::is_same<CT, BF16>::value) o[db] = M::mma(vf, pl, o[db]);
       }
     }
+  };
+
+  // the query rows land before the first tile copy is issued, so no wait in
+  // the loop has to cover them
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  if (nsteps > 0) issue_loads(0, 0);
+  if (nsteps > 1) issue_loads(1, 1);
+  for (int i0 = 0; i0 < nsteps; i0 += kPfStages) {
+#pragma unroll
+    for (int u = 0; u < kPfStages; ++u)
+      if (i0 + u < nsteps) step(i0 + u, u);
   }
 
   // ---- epilogue: O = O^T / l; lane holds dims DB*M + db for M in its 16 rows of O^T
@@ -302,6 +339,7 @@ __global__ __launch_bounds__(64 * kPfWaves, 2) void prefill_mfma_kernel(const Pr
     }
   }
 }
+
 
 template <class CT, int D>
 static void launch_one(const PrefillArgs& a, int max_q_len, hipStream_t s) {
