@@ -400,7 +400,7 @@ def main():
                 "unit": "TFLOP/s", "frac": round(achieved / MFMA_F16_PEAK_TFS, 4),
                 "traffic": _traffic(f"config{args.config}"),
                 "algorithmic_flops": int(wl.flops)}
-    roof["kernel"] = "decode_kernel + decode_reduce_kernel" if wl.bound == "hbm" else "prefill_kernel"
+    roof["kernel"] = "decode_kernel" if wl.bound == "hbm" else "prefill_mfma_kernel"
 
     cpu = None
     if args.cpu_budget > 0:

@@ -22,15 +22,19 @@
 // The S^T result layout (lane l: row l % 32, keys 8j + 4(l/32) + i) is the
 // P^T operand layout once each 16-key MFMA chunk takes keys {8j + 4(l/32) + i:
 // j in {2kc, 2kc+1}}, so probabilities never leave the lane.  V^T's operand
-// wants one head dim across 8 keys per lane: lane m reads head dims
-// [DB*m, DB*m + DB) of each key (DB = head_dim / 32) and PV MFMA db takes
-// element db of every key, so the dims land as DB*M + db.
+// wants one head dim across 8 keys per lane; ds_read_b64_tr_b16 delivers it
+// straight from the key-major V tile: within each group of 16 lanes, output
+// lane i receives element i % 4 of the 8 bytes addressed by lanes i / 4 + 4j
+// (j = 0..3), so lanes 4j + c address key j, dims 4c..4c+3, and lane i ends up
+// with dim i of keys 0..3 (layout measured on gfx950).
 //
-// LDS rows are 16-byte chunks XOR-swizzled by the key row (chunk j of row r at
-// position j ^ (r % chunks_per_row)); the global->LDS loads apply the inverse
-// permutation on the global side, so the per-lane LDS destinations stay the
-// hardware's consecutive ones, and both the K reads (16 keys x one chunk) and
-// the V reads (one key x all chunks) hit distinct banks.
+// LDS rows are 16-byte chunks XOR-swizzled per key row: K chunk j of row r sits
+// at position j ^ (r % chunks_per_row), so the K reads (16 keys x one chunk)
+// hit distinct banks; V chunk j sits at j ^ kVSwz[r % 4], which keeps the
+// transpose reads (4 keys x 4 chunks per 32 lanes, 4 keys x 2 chunks per 16)
+// conflict-free for 64 banks and for 32.  The global->LDS loads apply the
+// inverse permutation on the global side, so the per-lane LDS destinations
+// stay the hardware's consecutive ones.
 #include <type_traits>
 
 #include "hpa_attn_core.h"
@@ -40,6 +44,8 @@
 namespace hpa {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
 
 template <class CT> struct M32;
 template <> struct M32<F16> {
@@ -48,7 +54,11 @@ template <> struct M32<F16> {
                                                   c, 0, 0, 0);
   }
   __device__ __forceinline__ static uint32_t pack(float x, float y) {
-    return f32_to_f16_bits(x) | (f32_to_f16_bits(y) << 16);
+    return __builtin_bit_cast(uint32_t, (f16x2){(_Float16)x, (_Float16)y});  // v_cvt_pk_f16_f32, RNE
+  }
+  // acc + both halves of w, in fp32
+  __device__ __forceinline__ static float sum2(uint32_t w, float acc) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), (f16x2){1, 1}, acc, false);
   }
   __device__ __forceinline__ static float lo_of(uint32_t w) { return f16_bits_to_f32(w & 0xffffu); }
   __device__ __forceinline__ static float hi_of(uint32_t w) { return f16_bits_to_f32(w >> 16); }
@@ -59,7 +69,7 @@ template <> struct M32<BF16> {
                                                    c, 0, 0, 0);
   }
   __device__ __forceinline__ static uint32_t pack(float x, float y) {
-    return f32_to_bf16_bits(x) | (f32_to_bf16_bits(y) << 16);
+    return __builtin_bit_cast(uint32_t, (bf16x2){(__bf16)x, (__bf16)y});  // v_cvt_pk_bf16_f32, RNE
   }
   __device__ __forceinline__ static float lo_of(uint32_t w) { return bf16_bits_to_f32(w & 0xffffu); }
   __device__ __forceinline__ static float hi_of(uint32_t w) { return bf16_bits_to_f32(w >> 16); }
@@ -69,6 +79,17 @@ constexpr int kPfWaves = 4;              // waves per workgroup, 32 rows each
 constexpr int kPfRows = 32 * kPfWaves;   // rows per workgroup
 constexpr int kPfStages = 3;             // LDS tiles: two steps of loads in flight
 constexpr int kPfLazy = 8;               // rescale only when a row max grows by > 2^8
+
+// V-tile chunk swizzle by key row % 4 (chunks_per_row 16 and 8)
+__device__ __forceinline__ constexpr int v_swz(int nch, int row) {
+  return nch == 16 ? (row & 3) * 4 + ((row & 2) ? 2 : 0) : (row & 3) * 2;
+}
+
+// 4 x b16 transposed across each 16-lane group (see the layout above)
+__device__ __forceinline__ u32x2 lds_read_tr(const uint8_t* p) {
+  const i16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(p));
+  return __builtin_bit_cast(u32x2, r);
+}
 
 // x combined with the value of lane l ^ 32 (the other half of the same row)
 __device__ __forceinline__ float pair_max(float x) {
@@ -92,8 +113,7 @@ __global__ __launch_bounds__(64 * kPfWaves, 2) void prefill_mfma_kernel(const Pr
   constexpr int ROWB = D * 2;         // bytes per key row
   constexpr int TILEB = 32 * ROWB;    // one 32-key tile of K or of V
   constexpr int KCH = D / 16;         // QK MFMAs per step
-  constexpr int DB = D / 32;          // PV dim blocks; lane m holds dims [DB*m, DB*m + DB)
-  constexpr int VW = (DB * 2 + 3) / 4;  // u32 words of V per key per lane
+  constexpr int DB = D / 32;          // PV MFMAs per 16-key chunk: O^T block db = dims [32db, 32db + 32)
   constexpr int IPW = NCH / 4;        // global->LDS instructions per wave per step
   static_assert(D == 64 || D == 128, "head_dim 64 or 128");
   static_assert(kPfStages == 3, "the step loop is unrolled by three");
@@ -147,7 +167,8 @@ __global__ __launch_bounds__(64 * kPfWaves, 2) void prefill_mfma_kernel(const Pr
   for (int i = 0; i < IPW; ++i) {
     const int P = (w * IPW + i) * 64 + lane;     // chunk position in [K tile | V tile]
     const int row = (P % (32 * NCH)) / NCH, q = P % NCH;
-    voff[i] = (uint32_t)((row & 15) * ROWB + (q ^ (row % NCH)) * 16);
+    const int swz = tensor ? v_swz(NCH, row) : row % NCH;
+    voff[i] = (uint32_t)((row & 15) * ROWB + (q ^ swz) * 16);
   }
   const char* pool = reinterpret_cast<const char*>(tensor ? a.v : a.k);
   const long blk_rows = (long)a.num_kv_heads << a.bs_log2;   // key rows per block
@@ -180,21 +201,22 @@ __global__ __launch_bounds__(64 * kPfWaves, 2) void prefill_mfma_kernel(const Pr
   };
 
   // ---- per-lane LDS offsets of the operand reads (same in every stage)
-  uint32_t koff[KCH], vofs[2][8];
+  uint32_t koff[KCH], vofs[DB];
 #pragma unroll
   for (int c = 0; c < KCH; ++c) {
     const int jj = h * (NCH / 2) + c;
     koff[c] = (uint32_t)((n * NCH + (jj ^ (n % NCH))) * 16);
   }
   {
-    const int jv = (DB * 2 * n) / 16, off = (DB * 2 * n) % 16;
+    // transpose-read source lane 16g + 4j + c: key 4(g/2) + j (+ 8 per key
+    // group, an immediate), dims 32db + 16(g%2) + 4c
+    const int g = lane >> 4, j = (lane >> 2) & 3, c = lane & 3;
+    const int key = 4 * (g >> 1) + j;
 #pragma unroll
-    for (int kc = 0; kc < 2; ++kc)
-#pragma unroll
-      for (int s2 = 0; s2 < 8; ++s2) {
-        const int key = 8 * (2 * kc + (s2 >> 2)) + 4 * h + (s2 & 3);
-        vofs[kc][s2] = (uint32_t)(TILEB + (key * NCH + (jv ^ (key % NCH))) * 16 + off);
-      }
+    for (int db = 0; db < DB; ++db) {
+      const int ch = 4 * db + 2 * (g & 1) + (c >> 1);
+      vofs[db] = (uint32_t)(TILEB + key * ROWB + (ch ^ v_swz(NCH, key)) * 16 + 8 * (c & 1));
+    }
   }
 
   f32x16 o[DB];
@@ -228,20 +250,15 @@ __global__ __launch_bounds__(64 * kPfWaves, 2) void prefill_mfma_kernel(const Pr
     f32x16 st = (f32x16){};
 #pragma unroll
     for (int c = 0; c < KCH; ++c) st = M::mma(*reinterpret_cast<const u32x4*>(st_base + koff[c]), qf[c], st);
-    // ---- V rows of this lane's 16 keys, dims [DB*n, DB*n + DB)
-    uint32_t vr[2][8][VW];
+    // ---- V^T operands: dims 32db + l % 32, keys 8(2kc + r) + 4(l/32) + 0..3
+    u32x4 vf[2][DB];
 #pragma unroll
     for (int kc = 0; kc < 2; ++kc)
 #pragma unroll
-      for (int s2 = 0; s2 < 8; ++s2) {
-        const uint8_t* p = st_base + vofs[kc][s2];
-        if constexpr (VW == 2) {
-          const u32x2 x = *reinterpret_cast<const u32x2*>(p);
-          vr[kc][s2][0] = x[0];
-          vr[kc][s2][VW - 1] = x[1];
-        } else {
-          vr[kc][s2][0] = *reinterpret_cast<const uint32_t*>(p);
-        }
+      for (int db = 0; db < DB; ++db) {
+        const u32x2 lo = lds_read_tr(st_base + vofs[db] + (2 * kc) * 8 * ROWB);
+        const u32x2 hi = lds_read_tr(st_base + vofs[db] + (2 * kc + 1) * 8 * ROWB);
+        vf[kc][db] = (u32x4){lo[0], lo[1], hi[0], hi[1]};
       }
     // ---- online softmax over the row's 32 keys (16 here, 16 in lane ^ 32);
     // only steps crossing some row's limit pay for the mask
@@ -269,14 +286,9 @@ __global__ __launch_bounds__(64 * kPfWaves, 2) void prefill_mfma_kernel(const Pr
       for (int db = 0; db < DB; ++db) o[db] = o[db] * alpha;
     }
     const float mref = m == -INFINITY ? 0.f : m;
-    float ps = 0.f;
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(x[v], cs, -mref));
-      ps += p;
-      x[v] = p;  // -inf scores give exactly 0
-    }
-    l += ps;
+    for (int v = 0; v < 16; ++v)
+      x[v] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[v], cs, -mref));  // -inf scores give exactly 0
     // ---- O^T += V^T . P^T, two 16-key chunks
 #pragma unroll
     for (int kc = 0; kc < 2; ++kc) {
@@ -284,24 +296,23 @@ __global__ __launch_bounds__(64 * kPfWaves, 2) void prefill_mfma_kernel(const Pr
 #pragma unroll
       for (int p = 0; p < 4; ++p) pf[p] = M::pack(x[8 * kc + 2 * p], x[8 * kc + 2 * p + 1]);
       if constexpr (std::is_same<CT, BF16>::value) {
-        // bf16 keeps 8 significant bits; P = hi + lo carries ~16
+        // bf16 keeps 8 significant bits; P = hi + lo carries ~16, and the row
+        // sum takes the unrounded values
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
           const uint32_t wv = pf[p];
           pl[p] = M::pack(x[8 * kc + 2 * p] - M::lo_of(wv), x[8 * kc + 2 * p + 1] - M::hi_of(wv));
+          l += x[8 * kc + 2 * p] + x[8 * kc + 2 * p + 1];
         }
+      } else {
+        // the row sum of exactly the fp16 weights the MFMA multiplies
+#pragma unroll
+        for (int p = 0; p < 4; ++p) l = M::sum2(pf[p], l);
       }
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
-        const int wd = (db * 2) / 4, hb = db & 1;  // word and 16-bit half holding dim DB*n + db
-        const uint32_t sel = (uint32_t)(2 * hb) | ((uint32_t)(2 * hb + 1) << 8) |
-                             ((uint32_t)(4 + 2 * hb) << 16) | ((uint32_t)(5 + 2 * hb) << 24);
-        u32x4 vf;
-#pragma unroll
-        for (int p = 0; p < 4; ++p)
-          vf[p] = __builtin_amdgcn_perm(vr[kc][2 * p + 1][wd], vr[kc][2 * p][wd], sel);
-        o[db] = M::mma(vf, pf, o[db]);
-        if constexpr (std::is_same<CT, BF16>::value) o[db] = M::mma(vf, pl, o[db]);
+        o[db] = M::mma(vf[kc][db], pf, o[db]);
+        if constexpr (std::is_same<CT, BF16>::value) o[db] = M::mma(vf[kc][db], pl, o[db]);
       }
     }
   };
@@ -319,24 +330,22 @@ __global__ __launch_bounds__(64 * kPfWaves, 2) void prefill_mfma_kernel(const Pr
       if (i0 + u < nsteps) step(i0 + u, u);
   }
 
-  // ---- epilogue: O = O^T / l; lane holds dims DB*M + db for M in its 16 rows of O^T
+  // ---- epilogue: O = O^T / l; o[db][v] is dim 32db + 8(v/4) + 4h + v%4 of
+  // row n, so every 4 consecutive values are 4 consecutive dims
   const float lt = pair_sum(l);
   const float inv = lt > 0.f ? 1.f / lt : 0.f;
   if (rv) {
     const int t = r / G, hh = r - t * G;
-    q_t* orow = reinterpret_cast<q_t*>(a.out) + ((long)(q0 + t) * a.num_q_heads + kvh * G + hh) * D;
+    q_t* orow = reinterpret_cast<q_t*>(a.out) + ((long)(q0 + t) * a.num_q_heads + kvh * G + hh) * D + 4 * h;
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int Mi = 8 * (v >> 2) + 4 * h + (v & 3);
-      if constexpr (DB == 4) {
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int v4 = 0; v4 < 4; ++v4) {
         u32x2 pk;
-        pk[0] = M::pack(o[0][v] * inv, o[1][v] * inv);
-        pk[1] = M::pack(o[2][v] * inv, o[3][v] * inv);
-        *reinterpret_cast<u32x2*>(orow + DB * Mi) = pk;
-      } else {
-        *reinterpret_cast<uint32_t*>(orow + DB * Mi) = M::pack(o[0][v] * inv, o[1][v] * inv);
+        pk[0] = M::pack(o[db][4 * v4] * inv, o[db][4 * v4 + 1] * inv);
+        pk[1] = M::pack(o[db][4 * v4 + 2] * inv, o[db][4 * v4 + 3] * inv);
+        *reinterpret_cast<u32x2*>(orow + 32 * db + 8 * v4) = pk;
       }
-    }
   }
 }
 
