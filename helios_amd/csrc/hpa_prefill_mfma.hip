@@ -77,12 +77,31 @@ template <> struct M32<BF16> {
 
 constexpr int kPfWaves = 4;              // waves per workgroup, 32 rows each
 constexpr int kPfRows = 32 * kPfWaves;   // rows per workgroup
-constexpr int kPfStages = 3;             // LDS tiles: two steps of loads in flight
+constexpr int kPfStages = 4;             // LDS tiles: copies run kPfStages - 1 steps ahead
 constexpr int kPfLazy = 8;               // rescale only when a row max grows by > 2^8
 
 // V-tile chunk swizzle by key row % 4 (chunks_per_row 16 and 8)
 __device__ __forceinline__ constexpr int v_swz(int nch, int row) {
   return nch == 16 ? (row & 3) * 4 + ((row & 2) ? 2 : 0) : (row & 3) * 2;
+}
+
+constexpr int kPfLptMax = 512;           // items per XCD up to which workgroups run longest-first
+
+// Work item i is the (i / units)-th heaviest row tile of unit i % units.
+// Workgroups go to the 8 XCDs round-robin by id and, within an XCD, start in
+// id order as slots free up.  The workgroup with id 8m + x runs the item of
+// rank m -- by step count, longest first, ties by id -- among the items
+// 8j + x, so each XCD schedules its own items longest-first (list
+// scheduling's LPT rule) and a unit's tiles stay on one XCD's L2 whenever the
+// unit count is a multiple of 8.  Returns steps + 1, or 0 for an empty tile.
+__device__ __forceinline__ int item_cost(const PrefillArgs& a, int item, int units, int tiles) {
+  const int unit = item % units, tile = tiles - 1 - item / units;
+  const int b = unit / a.num_kv_heads;
+  const int rows = (a.cu_q[b + 1] - a.cu_q[b]) * a.group;
+  if (tile * kPfRows >= rows) return 0;
+  const int rlast = min(tile * kPfRows + kPfRows - 1, rows - 1);
+  const int lim = max(min(a.q_pos[b] + rlast / a.group + 1, a.ctx_lens[b]), 0);
+  return ((lim + 31) >> 5) + 1;
 }
 
 // 4 x b16 transposed across each 16-lane group (see the layout above)
@@ -116,14 +135,35 @@ __global__ __launch_bounds__(64 * kPfWaves, 2) void prefill_mfma_kernel(const Pr
   constexpr int DB = D / 32;          // PV MFMAs per 16-key chunk: O^T block db = dims [32db, 32db + 32)
   constexpr int IPW = NCH / 4;        // global->LDS instructions per wave per step
   static_assert(D == 64 || D == 128, "head_dim 64 or 128");
-  static_assert(kPfStages == 3, "the step loop is unrolled by three");
+  static_assert(kPfStages == 3 || kPfStages == 4, "waits below cover up to two later steps in flight");
   __shared__ __attribute__((aligned(16))) uint8_t smem[kPfStages][2 * TILEB];
 
-  // heaviest (last) row tiles first; the units of one tile index spread over
-  // consecutive workgroup ids, so a unit's tiles share an XCD when the unit
-  // count is a multiple of 8
-  const int unit = blockIdx.x;
-  const int tile = tiles_per_unit - 1 - (int)blockIdx.y;
+  // ---- which (unit, row tile) this workgroup runs: longest-first per XCD
+  const int units = a.num_seqs * a.num_kv_heads;
+  int item = (int)blockIdx.x;
+  {
+    __shared__ int s_pick;
+    const int xcd = item & 7, m = item >> 3;
+    const int nk = ((int)gridDim.x - xcd + 7) >> 3;  // items on this XCD
+    if (nk <= kPfLptMax) {
+      int* cost = reinterpret_cast<int*>(&smem[0][0]);
+      for (int j = threadIdx.x; j < nk; j += 64 * kPfWaves) cost[j] = item_cost(a, 8 * j + xcd, units, tiles_per_unit);
+      __syncthreads();
+      for (int j = threadIdx.x; j < nk; j += 64 * kPfWaves) {
+        const int cj = cost[j];
+        int rank = 0;
+        for (int i = 0; i < nk; ++i) {
+          const int ci = cost[i];
+          rank += (ci > cj) | ((ci == cj) & (i < j));
+        }
+        if (rank == m) s_pick = 8 * j + xcd;
+      }
+      __syncthreads();
+      item = __builtin_amdgcn_readfirstlane(s_pick);  // uniform: keeps everything below scalar
+    }
+  }
+  const int unit = item % units;
+  const int tile = tiles_per_unit - 1 - item / units;
   const int b = unit / a.num_kv_heads, kvh = unit - b * a.num_kv_heads;
   const int G = a.group;
   const int q0 = a.cu_q[b];
@@ -140,11 +180,13 @@ __global__ __launch_bounds__(64 * kPfWaves, 2) void prefill_mfma_kernel(const Pr
   const int r = r0 + n;                             // this lane's row
   const bool rv = r < rows;
   const int lim = rv ? limit(r) : 0;
+  // wave- and workgroup-uniform limits, pinned to scalar registers (the
+  // compiler would otherwise merge them with the per-lane limit above)
   const bool wave_live = r0 < rows;
-  const int wave_minlim = wave_live ? limit(r0) : 0;
-  const int wave_maxlim = wave_live ? limit(min(r0 + 31, rows - 1)) : 0;
+  const int wave_minlim = __builtin_amdgcn_readfirstlane(wave_live ? limit(r0) : 0);
+  const int wave_maxlim = __builtin_amdgcn_readfirstlane(wave_live ? limit(min(r0 + 31, rows - 1)) : 0);
   const int wg_maxlim = limit(min(tile * kPfRows + kPfRows - 1, rows - 1));
-  const int nsteps = (wg_maxlim + 31) >> 5;
+  const int nsteps = __builtin_amdgcn_readfirstlane((wg_maxlim + 31) >> 5);
 
   // ---- query rows into registers (B operand of S^T): lane half h holds dims
   // [h*D/2, (h+1)*D/2) as KCH chunks of 8
@@ -188,8 +230,11 @@ __global__ __launch_bounds__(64 * kPfWaves, 2) void prefill_mfma_kernel(const Pr
       if ((unsigned)phys >= (unsigned)a.num_blocks) { phys = 0; valid = 0; }
     }
     const char* base = pool + ((long)phys * blk_rows + head_rows + (key0 & bsm)) * ROWB;
+    // the record count is computed on the VALU (min/max); pinning it to a
+    // scalar keeps the resource uniform, with no per-lane loop around the loads
+    const int nbytes = __builtin_amdgcn_readfirstlane(valid * ROWB);
     const __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), (short)0, valid * ROWB, 0x00020000);
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), (short)0, nbytes, 0x00020000);
 #pragma unroll
     for (int i = 0; i < IPW; ++i) {
       // a local copy: the host pass of this builtin rejects a captured array
@@ -225,23 +270,29 @@ __global__ __launch_bounds__(64 * kPfWaves, 2) void prefill_mfma_kernel(const Pr
   float m = -INFINITY, l = 0.f;
   const float cs = a.scale_log2;
 
-  // one step: wait for its copies, barrier, issue the copies two steps ahead,
-  // then compute (STAGE folds to a constant in every unrolled call)
+  // one step: wait for its copies, barrier, issue the copies kPfStages - 1
+  // steps ahead, then compute (STAGE folds to a constant in every unrolled call)
   auto step = [&](int i, const int STAGE) {
-    if (i + 1 < nsteps) {
-      __builtin_amdgcn_s_waitcnt(0x0F70 | IPW);  // vmcnt(IPW): this wave's copies for step i landed
+    // this wave's copies for step i have landed once at most the later
+    // steps' groups (IPW loads each) are still in flight
+    const int later = min(nsteps - 1 - i, kPfStages - 2);
+    if (later >= 2) {
+      __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * IPW));  // vmcnt(2 IPW)
+    } else if (later == 1) {
+      __builtin_amdgcn_s_waitcnt(0x0F70 | IPW);        // vmcnt(IPW)
     } else {
-      __builtin_amdgcn_s_waitcnt(0x0F70);        // vmcnt(0)
+      __builtin_amdgcn_s_waitcnt(0x0F70);              // vmcnt(0)
     }
     // After the barrier every wave's copies for step i are in LDS (each
     // waited for its own above) and every wave has consumed its reads of
-    // the stage step i + 2 refills (step i - 1).  No memory fence: a
-    // workgroup fence would also wait for the copies of step i + 1 still in
-    // flight; the signal fences keep the compiler from moving LDS accesses.
+    // the stage that step i + kPfStages - 1 refills (step i - 1).  No memory
+    // fence: a workgroup fence would also wait for the later steps' copies
+    // still in flight; the signal fences keep the compiler from moving LDS
+    // accesses.
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_barrier();
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    if (i + 2 < nsteps) issue_loads(i + 2, (STAGE + 2) % kPfStages);
+    if (i + kPfStages - 1 < nsteps) issue_loads(i + kPfStages - 1, (STAGE + kPfStages - 1) % kPfStages);
     const int k0 = 32 * i;
     if (k0 >= wave_maxlim) return;
     const uint8_t* st_base = &smem[STAGE][0];
@@ -322,8 +373,9 @@ __global__ __launch_bounds__(64 * kPfWaves, 2) void prefill_mfma_kernel(const Pr
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  if (nsteps > 0) issue_loads(0, 0);
-  if (nsteps > 1) issue_loads(1, 1);
+#pragma unroll
+  for (int u = 0; u < kPfStages - 1; ++u)
+    if (u < nsteps) issue_loads(u, u);
   for (int i0 = 0; i0 < nsteps; i0 += kPfStages) {
 #pragma unroll
     for (int u = 0; u < kPfStages; ++u)
@@ -354,7 +406,7 @@ template <class CT, int D>
 static void launch_one(const PrefillArgs& a, int max_q_len, hipStream_t s) {
   const int units = a.num_seqs * a.num_kv_heads;
   const int tiles = (max_q_len * a.group + kPfRows - 1) / kPfRows;
-  hipLaunchKernelGGL((prefill_mfma_kernel<CT, D>), dim3((unsigned)units, (unsigned)tiles), dim3(64 * kPfWaves),
+  hipLaunchKernelGGL((prefill_mfma_kernel<CT, D>), dim3((unsigned)(units * tiles)), dim3(64 * kPfWaves),
                      0, s, a, a.tables, tiles);
 }
 
@@ -362,6 +414,8 @@ bool launch_prefill_mfma(const PrefillArgs& a, int q_dtype, int kv_dtype, int he
                          hipStream_t s) {
   if (a.bs_log2 < 4 || kv_dtype != q_dtype || (head_dim != 64 && head_dim != 128)) return false;
   if ((long)max_q_len * a.group > (1L << 30)) return false;
+  if ((long)a.num_seqs * a.num_kv_heads * ((max_q_len * (long)a.group + kPfRows - 1) / kPfRows) > 0x7fffffffL)
+    return false;
   if (q_dtype == HPA_F16) {
     if (head_dim == 128) launch_one<F16, 128>(a, max_q_len, s);
     else launch_one<F16, 64>(a, max_q_len, s);
