@@ -321,8 +321,10 @@ def _traffic(workload_key):
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=200)
+    # the GPU clock takes tens of milliseconds of sustained work to ramp up;
+    # a short warmup understates the steady-state rate by up to ~20%
+    ap.add_argument("--warmup", type=int, default=500)
     ap.add_argument("--config", type=int, default=5, choices=[1, 2, 3, 4, 5])
     ap.add_argument("--seed", type=int, default=None)
     ap.add_argument("--part-tokens", type=int, default=0,
