@@ -140,7 +140,7 @@ class DecodeWorkload(Workload):
             self.new_k = torch.randn(B, Hkv, D, generator=gen, device=device, dtype=dtype)
             self.new_v = torch.randn(B, Hkv, D, generator=gen, device=device, dtype=dtype)
             self.new_pos = torch.tensor([c - 1 for c in lens], dtype=torch.int32, device=device)
-            self.ones = [1] * B
+            self.new_cu = torch.arange(0, B + 1, dtype=torch.int32, device=device)
         self.i = 0
         kvb = D * (1 if quant else (4 if cfg == 1 else 2)) + (2 if quant else 0)
         elt = 4 if cfg == 1 else 2
@@ -159,7 +159,8 @@ class DecodeWorkload(Workload):
         c = self.caches[self.i % len(self.caches)]
         self.i += 1
         if self.cfg == 3:
-            H.write_kv(c, self.tables_t, self.new_pos, self.new_k, self.new_v, query_lens=self.ones)
+            H.write_kv(c, self.tables_t, self.new_pos, self.new_k, self.new_v,
+                       cu_query_lens=self.new_cu, max_query_len=1)
         ks, vs = c._scales()
         H.paged_attention_decode_hip(
             self.q, c.k_cache, c.v_cache, self.tables_t, self.lens_t, self.scale, ks, vs,

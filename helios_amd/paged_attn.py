@@ -211,12 +211,17 @@ def write_kv(
     k: torch.Tensor,
     v: torch.Tensor,
     query_lens: Optional[LensArg] = None,
+    cu_query_lens: Optional[torch.Tensor] = None,
+    max_query_len: Optional[int] = None,
 ) -> None:
     """Scatter (fp) or quantize-and-scatter (int8) K/V of a ragged batch in
     one launch.  k, v: [sum(query_lens), n_kv_heads, head_dim]; sequence b's
     tokens go to positions start_positions[b].. through block_tables[b].
-    With one sequence and no query_lens, every token belongs to it.  Table
-    entries are not bounds-checked here (PagedKVCache.write checks them)."""
+    With one sequence and no query_lens, every token belongs to it.  A caller
+    that keeps int32 device metadata passes cu_query_lens ([n + 1] offsets)
+    and max_query_len instead of query_lens, and the call does no host work
+    beyond the launch.  Table entries are not bounds-checked here
+    (PagedKVCache.write checks them)."""
     _require_gpu(k, "k")
     dev = kv_cache.k_cache.device
     if isinstance(block_tables, torch.Tensor):
@@ -225,14 +230,22 @@ def write_kv(
     else:
         n_seqs = len(block_tables)
         tables = _padded_tables(block_tables, dev)
-    if query_lens is None:
-        if n_seqs != 1:
-            raise ValueError("query_lens is required for more than one sequence")
-        query_lens = [k.shape[0]]
-    qlens = [int(x) for x in (query_lens.tolist() if isinstance(query_lens, torch.Tensor) else query_lens)]
-    cu = [0]
-    for x in qlens:
-        cu.append(cu[-1] + x)
+    if cu_query_lens is not None:
+        if max_query_len is None:
+            raise ValueError("max_query_len is required with cu_query_lens")
+        if cu_query_lens.dtype != torch.int32 or cu_query_lens.numel() != n_seqs + 1:
+            raise ValueError("cu_query_lens must be int32 [n_seqs + 1]")
+        cu_t, max_q = cu_query_lens, int(max_query_len)
+    else:
+        if query_lens is None:
+            if n_seqs != 1:
+                raise ValueError("query_lens is required for more than one sequence")
+            query_lens = [k.shape[0]]
+        qlens = [int(x) for x in (query_lens.tolist() if isinstance(query_lens, torch.Tensor) else query_lens)]
+        cu = [0]
+        for x in qlens:
+            cu.append(cu[-1] + x)
+        cu_t, max_q = _i32(cu, dev), (max(qlens) if qlens else 0)
     starts = start_positions if isinstance(start_positions, torch.Tensor) else _i32(list(start_positions), dev)
     k = k.contiguous()
     v = v.contiguous()
@@ -241,7 +254,7 @@ def write_kv(
         ptr(k), ptr(v), DTYPE_CODE[k.dtype], ptr(kv_cache.k_cache), ptr(kv_cache.v_cache),
         DTYPE_CODE[kv_cache.pool_dtype], ptr(ks), ptr(vs),
         DTYPE_CODE[ks.dtype] if ks is not None else 0, ptr(tables), tables.shape[1],
-        ptr(_i32(cu, dev)), ptr(starts), n_seqs, max(qlens) if qlens else 0,
+        ptr(cu_t), ptr(starts), n_seqs, max_q,
         kv_cache.n_kv_heads, kv_cache.head_dim, kv_cache.block_size, kv_cache.num_blocks,
         stream_ptr(dev),
     )

@@ -67,6 +67,32 @@ def test_config3_new_token_write_per_sequence():
     assert np.array_equal(to_np(cache.v_scale), pool.v_scale)
 
 
+def test_write_with_device_offsets_matches_list_lengths():
+    """write_kv with int32 device offsets (cu_query_lens + max_query_len, no
+    host work) writes exactly what the list form writes, ragged lengths and
+    an empty sequence included."""
+    gen = torch.Generator().manual_seed(5)
+    H, D, bs, nb = 2, 64, 16, 48
+    qlens = [3, 0, 5, 1, 17]
+    starts = [13, 40, 0, 31, 2]
+    perm = np.random.default_rng(5).permutation(nb)
+    tables = [[int(x) for x in perm[8 * i:8 * i + 8]] for i in range(len(qlens))]
+    k = torch.randn(sum(qlens), H, D, generator=gen).half().cuda()
+    v = torch.randn(sum(qlens), H, D, generator=gen).half().cuda()
+    a = QuantizedPagedKVCache(nb, bs, H, D, dtype=torch.float16, device="cuda")
+    b = QuantizedPagedKVCache(nb, bs, H, D, dtype=torch.float16, device="cuda")
+    write_kv(a, tables, starts, k, v, query_lens=qlens)
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(qlens)]), dtype=torch.int32, device="cuda")
+    tab = torch.tensor(tables, dtype=torch.int32, device="cuda")
+    st = torch.tensor(starts, dtype=torch.int32, device="cuda")
+    write_kv(b, tab, st, k, v, cu_query_lens=cu, max_query_len=max(qlens))
+    torch.cuda.synchronize()
+    for x, y in ((a.k_cache, b.k_cache), (a.v_cache, b.v_cache), (a.k_scale, b.k_scale), (a.v_scale, b.v_scale)):
+        assert torch.equal(x, y)
+    with pytest.raises(ValueError):
+        write_kv(b, tab, st, k, v, cu_query_lens=cu)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 def test_fp_write_and_gather_round_trip(dtype):
     """reference tests/parity/test_parity.py:134-142 on the device."""
