@@ -119,31 +119,27 @@ __device__ int total_steps_per_head(const DecodeArgs& a) {
   return wave_sum_i(acc);
 }
 
-// The unit whose cost range holds global position s0 (< total).  A unit's
-// range is kUnitCost positions of overhead followed by its steps.
-// Wave-uniform result.
+// The sequence whose cost range in one KV head's position space holds s0
+// (< total).  A sequence's range is kUnitCost positions of overhead followed
+// by its steps.  Wave-uniform result; the caller sets the head.
 __device__ UnitPos locate(const DecodeArgs& a, int s0) {
   const int lane = threadIdx.x & 63;
-  const int H = a.num_kv_heads;
-  int run = 0;  // steps per head before this chunk
+  int run = 0;  // positions before this chunk
   UnitPos p{0, 0, 1, 0};
   for (int base = 0; base < a.num_seqs; base += 64) {
     const int b = base + lane;
     const int n = b < a.num_seqs ? unit_steps(a.ctx_lens[b], a.max_ctx) : 0;
     const int c = b < a.num_seqs ? n + kUnitCost : 0;
     const int incl = wave_incl_scan_i(c);
-    const int first = H * (run + incl - c);  // global first position of sequence b
-    const int last = H * (run + incl);       // one past its last
+    const int first = run + incl - c;  // first position of sequence b
+    const int last = run + incl;       // one past its last
     const unsigned long long hit =
         __builtin_amdgcn_ballot_w64(b < a.num_seqs && first <= s0 && s0 < last);
     if (hit) {
       const int l = __builtin_ffsll((long long)hit) - 1;
-      const int fb = __builtin_amdgcn_readfirstlane(__shfl(first, l));
-      const int nb = __builtin_amdgcn_readfirstlane(__shfl(n, l));
       p.b = base + l;
-      p.n = nb;
-      p.kvh = (s0 - fb) / (nb + kUnitCost);
-      p.g = fb + p.kvh * (nb + kUnitCost);
+      p.n = __builtin_amdgcn_readfirstlane(__shfl(n, l));
+      p.g = __builtin_amdgcn_readfirstlane(__shfl(first, l));
       return p;
     }
     run += __builtin_amdgcn_readfirstlane(__shfl(incl, 63));
@@ -174,13 +170,21 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
   const q_t* q = reinterpret_cast<const q_t*>(a.q);
   q_t* out = reinterpret_cast<q_t*>(a.out);
 
-  // ---- this wave's slice [s0, s1) of the global step range
-  const int total = __builtin_amdgcn_readfirstlane(H * total_steps_per_head(a));
-  const int per = max(a.min_steps, (total + a.num_waves - 1) / a.num_waves);
-  const int s0 = wave * per;
+  // ---- this wave's slice.  Waves form groups of H; a group takes the slice
+  // [s0, s1) of one KV head's position space (sequences laid end to end)
+  // and wave h of the group runs KV head h of it.  The H waves of a group
+  // walk the same blocks at the same pace, so each block's K (and V) rows
+  // of all heads -- one contiguous run of H slabs -- are fetched together.
+  const int NG = max(1, a.num_waves / H);
+  const int grp = wave / H, head = wave - grp * H;
+  if (grp >= NG) return;
+  const int total = __builtin_amdgcn_readfirstlane(total_steps_per_head(a));
+  const int per = max(a.min_steps, (total + NG - 1) / NG);
+  const int s0 = grp * per;
   if (s0 >= total) return;
   const int s1 = min(total, s0 + per);
   UnitPos u = locate(a, s0);
+  u.kvh = head;
 
   const typename Core::LaneOff lo = Core::lane_off();
   int ls = max(s0 - (u.g + kUnitCost), 0);  // first local step of the unit in the slice
@@ -278,7 +282,7 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
                 (uint32_t)((slot * a.rows + r) * 8), 0, kCoherent);
         }
       }
-      const int wa = sb / per, wb = (sb + u.n - 1) / per;  // waves holding the pieces
+      const int wa = sb / per, wb = (sb + u.n - 1) / per;  // groups holding the pieces
       const int unit = u.b * H + u.kvh;
       // the piece's stores are complete (hence visible device-wide) before
       // the counter moves
@@ -293,8 +297,9 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
         // the workspace (this wave's own included), so every merging wave
         // evaluates the same expression
         if (lane == 0) __hip_atomic_store(a.counters + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        // wave wa saw this unit first iff its slice began inside the unit's range
-        const long slot_a = 2L * wa + (wa * per >= u.g ? 0 : 1);
+        // group wa saw this unit first iff its slice began inside the unit's
+        // range; the piece of group p sits in the slots of wave p H + head
+        const long slot_a = 2L * (wa * H + head) + (wa * per >= u.g ? 0 : 1);
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
           const int r = nt * 16 + n;
@@ -307,7 +312,7 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
           for (int e = 0; e < 4 * J; ++e) acc[e] = 0.f;
 #pragma unroll 2
           for (int p = wa; p <= wb; ++p) {
-            const long sl = p == wa ? slot_a : 2L * p;
+            const long sl = p == wa ? slot_a : 2L * (p * H + head);
             const u32x2 ml = __builtin_amdgcn_raw_buffer_load_b64(rml, (uint32_t)((sl * a.rows + r) * 8), 0, kCoherent);
             const uint32_t ob = (uint32_t)(((sl * a.rows + r) * D + 4 * J * g) * 4);
             u32x4 ov[J];
@@ -364,15 +369,10 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
     }
 
     if (sb + lend >= s1) break;
-    // next unit: (b, kvh + 1) or (b + 1, 0)
+    // next unit: the next sequence, same head
     u.g += u.n + kUnitCost;
-    if (u.kvh + 1 < H) {
-      ++u.kvh;
-    } else {
-      ++u.b;
-      u.kvh = 0;
-      u.n = unit_steps(__builtin_amdgcn_readfirstlane(a.ctx_lens[u.b]), a.max_ctx);
-    }
+    ++u.b;
+    u.n = unit_steps(__builtin_amdgcn_readfirstlane(a.ctx_lens[u.b]), a.max_ctx);
     ls = 0;
     first_unit = false;
   }
@@ -408,7 +408,12 @@ int launch_decode_kernel(DecodeArgs& a, int cap, hipStream_t s) {
     groups_per_cu = nb;
   }
   const long resident = (long)device_cus() * groups_per_cu * kWavesPerGroup;
-  a.num_waves = (int)std::max(1L, std::min<long>(cap, resident));
+  // whole groups of num_kv_heads waves, at least one; a single group never
+  // cuts a unit, so it needs no workspace slots even when cap is smaller
+  const long H = a.num_kv_heads;
+  long nw = std::min<long>(cap, resident);
+  nw = std::max(H, nw - nw % H);
+  a.num_waves = (int)nw;
   const unsigned groups = (unsigned)((a.num_waves + kWavesPerGroup - 1) / kWavesPerGroup);
   hipLaunchKernelGGL((decode_kernel<CT, KVT, ST, D, NT, BIG>), dim3(groups), dim3(64 * kWavesPerGroup),
                      0, s, a);
