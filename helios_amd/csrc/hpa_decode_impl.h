@@ -187,20 +187,37 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
   u.kvh = head;
 
   const typename Core::LaneOff lo = Core::lane_off();
-  int ls = max(s0 - (u.g + kUnitCost), 0);  // first local step of the unit in the slice
+  constexpr int NB = kDepth + 1;
+  // A ring of kDepth + 1 register buffers, unrolled so every index is a
+  // compile-time constant: kDepth steps of loads stay in flight while a step
+  // computes, and no buffer is ever copied (a register copy of data still in
+  // flight would make the compiler wait for it).
+  typename Core::Raw rb[NB];
+  auto make_pv = [&](const UnitPos& uu, int c) -> PoolView {
+    return PoolView{a.k, a.v, a.ks, a.vs, a.tables + (long)uu.b * a.table_stride, a.table_stride,
+                    uu.kvh, H, a.bs_log2, a.num_blocks, c};
+  };
+  auto unit_ctx = [&](const UnitPos& uu) -> int {
+    return min(__builtin_amdgcn_readfirstlane(a.ctx_lens[uu.b]), a.max_ctx);
+  };
+
+  // ---- the first unit: window and the first kDepth steps of loads
+  int lbeg = max(s0 - (u.g + kUnitCost), 0);  // first local step of the unit in the slice
+  int ctx = unit_ctx(u);
+  int sb = u.g + kUnitCost;  // global position of the unit's step 0
+  int lend = min(u.n, s1 - sb);  // steps of this unit in the slice: [lbeg, lend)
+  if (lend <= lbeg) return;  // the slice ends inside the unit's overhead: the next group has it
+  PoolView pv = make_pv(u, ctx);
+  TableWindow win;
+  if (BIG && ctx > 0) win.fill(pv.table, pv.table_stride, (32 * lbeg) >> a.bs_log2);  // waited on at first use
+  if (ctx > 0) {
+#pragma unroll
+    for (int k = 0; k < kDepth; ++k)
+      Core::template load_sel<BIG>(pv, win, 32 * (lbeg + k), lo, rb[k], lbeg + k < lend);
+  }
   bool first_unit = true;
 
   for (;;) {
-    const int ctx = min(__builtin_amdgcn_readfirstlane(a.ctx_lens[u.b]), a.max_ctx);
-    const int sb = u.g + kUnitCost;  // global position of the unit's step 0
-    const int lbeg = ls;
-    const int lend = min(u.n, s1 - sb);  // steps of this unit in the slice: [lbeg, lend)
-    if (lend <= lbeg) break;  // the slice ends inside the unit's overhead: the next wave has it
-    const PoolView pv{a.k, a.v, a.ks, a.vs, a.tables + (long)u.b * a.table_stride, a.table_stride,
-                      u.kvh, H, a.bs_log2, a.num_blocks, ctx};
-    TableWindow win;
-    if (BIG && ctx > 0) win.fill(pv.table, pv.table_stride, (32 * lbeg) >> a.bs_log2);  // waited on at first use
-
     // ---- unit prologue: query rows of (u.b, u.kvh)
     auto out_row = [&](int r) -> long {
       const int t = r / G, hh = r - t * G;
@@ -223,17 +240,8 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
     Core core;
     core.init(rowq, rowlim);
 
-    // ---- stream the unit's steps [lbeg, lend) with one step in flight
+    // ---- stream the unit's steps [lbeg, lend); the first kDepth are in flight
     if (ctx > 0) {
-      // A ring of kDepth + 1 register buffers, unrolled so every index is a
-      // compile-time constant: kDepth steps of loads stay in flight while a
-      // step computes, and no buffer is ever copied (a register copy of data
-      // still in flight would make the compiler wait for it).
-      constexpr int NB = kDepth + 1;
-      typename Core::Raw rb[NB];
-#pragma unroll
-      for (int k = 0; k < kDepth; ++k)
-        Core::template load_sel<BIG>(pv, win, 32 * (lbeg + k), lo, rb[k], lbeg + k < lend);
       bool done = false;
       for (int st = lbeg; !done; st += NB) {
 #pragma unroll
@@ -248,6 +256,29 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
         }
       }
     }
+
+    // ---- the next unit (the next sequence, same head), started before this
+    // unit's epilogue so that its loads overlap the epilogue's latency
+    const bool has_next = sb + lend < s1;
+    UnitPos un = u;
+    int ctx_n = 0, lend_n = 0;
+    TableWindow win_n;
+    if (has_next) {
+      un.g += u.n + kUnitCost;
+      ++un.b;
+      un.n = unit_steps(__builtin_amdgcn_readfirstlane(a.ctx_lens[un.b]), a.max_ctx);
+      ctx_n = unit_ctx(un);
+      lend_n = min(un.n, s1 - (un.g + kUnitCost));
+      if (BIG && ctx_n > 0 && lend_n > 0) win_n.fill(a.tables + (long)un.b * a.table_stride, a.table_stride, 0);
+    }
+    const PoolView pv_n = make_pv(un, ctx_n);
+    auto prime_next = [&]() {
+      if (has_next && ctx_n > 0 && lend_n > 0) {
+#pragma unroll
+        for (int k = 0; k < kDepth; ++k)
+          Core::template load_sel<BIG>(pv_n, win_n, 32 * k, lo, rb[k], k < lend_n);
+      }
+    };
 
     // ---- unit epilogue
     float lrow[NT];
@@ -291,6 +322,8 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
       __atomic_signal_fence(__ATOMIC_SEQ_CST);
       int old = 0;
       if (lane == 0) old = __hip_atomic_fetch_add(a.counters + unit, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // the next unit's loads go out while the count comes back
+      prime_next();
       old = __builtin_amdgcn_readfirstlane(old);
       if (old == wb - wa) {
         // last piece: merge every piece in piece order, all read back from
@@ -351,6 +384,7 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
         }
       }
     } else {
+      prime_next();
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         const int r = nt * 16 + n;
@@ -368,12 +402,14 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
       }
     }
 
-    if (sb + lend >= s1) break;
-    // next unit: the next sequence, same head
-    u.g += u.n + kUnitCost;
-    ++u.b;
-    u.n = unit_steps(__builtin_amdgcn_readfirstlane(a.ctx_lens[u.b]), a.max_ctx);
-    ls = 0;
+    if (!has_next || lend_n <= 0) break;
+    u = un;
+    ctx = ctx_n;
+    sb = un.g + kUnitCost;
+    lbeg = 0;
+    lend = lend_n;
+    pv = pv_n;
+    win = win_n;
     first_unit = false;
   }
 }
