@@ -137,3 +137,51 @@ def test_rows_without_keys_are_zero():
     # context 0: nothing to attend
     got = paged_attention_varlen(q, cache, tables, [3], [0], [0])
     assert torch.count_nonzero(got) == 0
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,bs,dtype", [
+    (14, 2, 64, 16, torch.float16),    # Qwen2.5-0.5B heads: group of 7 rows per token
+    (14, 2, 64, 32, torch.bfloat16),
+    (8, 8, 128, 64, torch.float16),    # group of 1
+    (32, 4, 128, 16, torch.bfloat16),  # group of 8
+])
+def test_mfma_prefill_group_and_block_shapes(Hq, Hkv, D, bs, dtype):
+    """The fp16/bf16 MFMA kernel packs the group's query heads into 128-row
+    tiles; row tiles then end mid-token for groups that do not divide 128."""
+    qlens = [1, 37, 130, 9]
+    starts = [3, 0, 250, 64]
+    ctxs = [s + n for s, n in zip(starts, qlens)]
+    cache, tables, gen = _setup(Hq + bs, ctxs, Hq, Hkv, D, bs, dtype)
+    q = torch.randn(sum(qlens), Hq, D, generator=gen).to(dtype).to(dev())
+    got = paged_attention_varlen(q, cache, tables, qlens, starts, ctxs)
+    want = R.paged_varlen(to_np(q).astype(np.float32), pool_of(cache), tables, qlens, starts, ctxs)
+    _check(got, want, dtype, f"Hq={Hq} Hkv={Hkv} D={D} bs={bs}")
+
+
+def test_mfma_prefill_context_shorter_than_chunk():
+    """context_len below start + n caps every row's keys at the context
+    (paged_attn.py:401-404 with the gather cut at context_len)."""
+    qlens = [20, 6]
+    starts = [40, 0]
+    ctxs = [45, 3]
+    cache, tables, gen = _setup(21, [60, 6], 16, 4, 128, 16, torch.float16)
+    q = torch.randn(sum(qlens), 16, 128, generator=gen).half().to(dev())
+    got = paged_attention_varlen(q, cache, tables, qlens, starts, ctxs)
+    want = R.paged_varlen(to_np(q).astype(np.float32), pool_of(cache), tables, qlens, starts, ctxs)
+    _check(got, want, torch.float16)
+
+
+@pytest.mark.parametrize("n_seqs", [100, 520])
+def test_mfma_prefill_many_small_sequences(n_seqs):
+    """Many (sequence, KV head) items: 100 sequences keep the longest-first
+    order of each XCD's items; 520 x 8 heads exceed the 512 items per XCD it
+    ranks and run in dispatch order.  Every row is checked."""
+    rng = np.random.default_rng(n_seqs)
+    qlens = [int(x) for x in rng.integers(1, 5, size=n_seqs)]
+    ctxs = [int(x) for x in rng.integers(1, 61, size=n_seqs)]
+    starts = [max(c - n, 0) for c, n in zip(ctxs, qlens)]
+    cache, tables, gen = _setup(n_seqs, ctxs, 32, 8, 128, 16, torch.float16)
+    q = torch.randn(sum(qlens), 32, 128, generator=gen).half().to(dev())
+    got = paged_attention_varlen(q, cache, tables, qlens, starts, ctxs)
+    want = R.paged_varlen(to_np(q).astype(np.float32), pool_of(cache), tables, qlens, starts, ctxs)
+    _check(got, want, torch.float16, f"{n_seqs} sequences")
