@@ -64,6 +64,12 @@ SIGNATURES = {
          _c_ptr, _c_int, _c_ptr, _c_ptr, _c_int, _c_int, _c_int, _c_int, _c_int,
          _c_int, _c_ptr],
     ),
+    "hpa_kv_write_rope": (
+        _c_int,
+        [_c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_int,
+         _c_ptr, _c_int, _c_ptr, _c_ptr, _c_int, _c_int, _c_int, _c_int, _c_int,
+         _c_int, _c_ptr, _c_ptr, _c_int, _c_ptr],
+    ),
     "hpa_kv_gather": (
         _c_int,
         [_c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_int, _c_ptr, _c_int, _c_ptr,

@@ -33,11 +33,39 @@ struct WriteArgs {
   const int32_t* cu_tokens;
   const int32_t* start_pos;
   int num_kv_heads, head_dim, bs_log2, num_blocks;
+  // optional rotary tables [rope_rows][head_dim / 2] (fp32); K is rotated by
+  // its write position when rope_cos is set
+  const float* rope_cos;
+  const float* rope_sin;
+  int rope_rows;
 };
+
+// Element d of K rotated rotate-half style at position pos (reference
+// exec/model.py:135-153): with c, s = cos/sin[pos][d mod D/2],
+//   d <  D/2: x[d] c - x[d + D/2] s       d >= D/2: x[d] c + x[d - D/2] s
+// Each product and the sum are rounded to fp32 separately, as torch's
+// separate elementwise ops round them: contraction into a fused multiply-add
+// (which HIP allows by default, also through __fmul_rn) is switched off here.
+template <class IT>
+__device__ __forceinline__ float rope_elem(const typename IT::storage* x, int d, int D, const float* cs_row,
+                                           const float* sn_row) {
+#pragma clang fp contract(off)
+  const int half = D >> 1;
+  const int j = d < half ? d : d - half;
+  const float c = cs_row[j], sn = sn_row[j];
+  const float xd = Cvt<IT>::to_f32(x[d]);
+  if (d < half) {
+    const float xo = Cvt<IT>::to_f32(x[d + half]);
+    return xd * c - xo * sn;
+  }
+  const float xo = Cvt<IT>::to_f32(x[d - half]);
+  return xd * c + xo * sn;
+}
 
 __device__ __forceinline__ long write_slot(const WriteArgs& a, int b, int i, int h) {
   const int pos = a.start_pos[b] + i;
   if (pos < 0) return -1;
+  if (a.rope_cos && pos >= a.rope_rows) return -1;  // no rotary row for it
   const int lb = pos >> a.bs_log2;
   if (lb >= a.table_stride) return -1;
   const int phys = a.tables[(long)b * a.table_stride + lb];
@@ -62,7 +90,13 @@ __global__ __launch_bounds__(256) void kv_write_fp_kernel(const WriteArgs a, int
     const long src = (long)(t0 + i) * per_tok + rem;
     typedef typename IT::storage i_t;
     typedef typename PT::storage p_t;
-    const float kx = Cvt<IT>::to_f32(reinterpret_cast<const i_t*>(a.k)[src]);
+    float kx;
+    if (a.rope_cos) {
+      const long row = (long)(a.start_pos[b] + i) * (D >> 1);
+      kx = rope_elem<IT>(reinterpret_cast<const i_t*>(a.k) + (src - d), d, D, a.rope_cos + row, a.rope_sin + row);
+    } else {
+      kx = Cvt<IT>::to_f32(reinterpret_cast<const i_t*>(a.k)[src]);
+    }
     const float vx = Cvt<IT>::to_f32(reinterpret_cast<const i_t*>(a.v)[src]);
     reinterpret_cast<p_t*>(a.kp)[slot * D + d] = Cvt<PT>::from_f32(kx);
     reinterpret_cast<p_t*>(a.vp)[slot * D + d] = Cvt<PT>::from_f32(vx);
@@ -79,14 +113,15 @@ __device__ __forceinline__ float wave_max(float x) {
 // head_dim elements [l*EPL, l*EPL + EPL).
 template <class IT, class ST, int EPL>
 __device__ __forceinline__ void quant_one(const typename IT::storage* x, int8_t* qdst,
-                                          typename ST::storage* sdst, int D) {
+                                          typename ST::storage* sdst, int D, const float* cs_row = nullptr,
+                                          const float* sn_row = nullptr) {
   const int lane = threadIdx.x & 63;
   float v[EPL];
   float amax = 0.f;
 #pragma unroll
   for (int e = 0; e < EPL; ++e) {
     const int d = lane * EPL + e;
-    v[e] = d < D ? Cvt<IT>::to_f32(x[d]) : 0.f;
+    v[e] = d < D ? (cs_row ? rope_elem<IT>(x, d, D, cs_row, sn_row) : Cvt<IT>::to_f32(x[d])) : 0.f;
     amax = fmaxf(amax, fabsf(v[e]));
   }
   amax = wave_max(amax);
@@ -122,9 +157,11 @@ __global__ __launch_bounds__(256) void kv_write_i8_kernel(const WriteArgs a) {
   typedef typename IT::storage i_t;
   typedef typename ST::storage s_t;
   const long src = ((long)(t0 + i) * H + h) * D;
+  const long row = (long)(a.start_pos[b] + i) * (D >> 1);
   quant_one<IT, ST, EPL>(reinterpret_cast<const i_t*>(a.k) + src,
                          reinterpret_cast<int8_t*>(a.kp) + slot * D,
-                         reinterpret_cast<s_t*>(a.ks) + slot, D);
+                         reinterpret_cast<s_t*>(a.ks) + slot, D, a.rope_cos ? a.rope_cos + row : nullptr,
+                         a.rope_cos ? a.rope_sin + row : nullptr);
   quant_one<IT, ST, EPL>(reinterpret_cast<const i_t*>(a.v) + src,
                          reinterpret_cast<int8_t*>(a.vp) + slot * D,
                          reinterpret_cast<s_t*>(a.vs) + slot, D);
@@ -253,34 +290,62 @@ static int launch_gather_out(const GatherArgs& a, int out_dtype, hipStream_t s) 
 
 using namespace hpa;
 
+static int kv_write_impl(const char* who, const void* k, const void* v, int in_dtype, void* k_pool,
+                         void* v_pool, int pool_dtype, void* k_scale, void* v_scale, int scale_dtype,
+                         const int32_t* block_tables, int table_stride, const int32_t* cu_tokens,
+                         const int32_t* start_positions, int num_seqs, int max_tokens, int num_kv_heads,
+                         int head_dim, int block_size, int num_blocks, const float* rope_cos,
+                         const float* rope_sin, int rope_rows, hipStream_t stream) {
+  if (num_seqs == 0 || max_tokens == 0) return HPA_OK;
+  if (!k || !v || !k_pool || !v_pool || !block_tables || !cu_tokens || !start_positions)
+    return fail(HPA_ERR_ARG, "%s: null pointer argument", who);
+  if (rope_cos && (!rope_sin || rope_rows <= 0 || (head_dim & 1)))
+    return fail(HPA_ERR_ARG, "%s: rotary tables need sin, rows > 0 and an even head_dim", who);
+  if (num_seqs < 0 || max_tokens < 0 || num_kv_heads <= 0 || head_dim <= 0 || table_stride <= 0 ||
+      num_blocks <= 0)
+    return fail(HPA_ERR_ARG, "%s: bad shape", who);
+  const int bsl = ilog2_exact(block_size);
+  if (bsl < 0 || bsl > 10)
+    return fail(HPA_ERR_UNSUPPORTED, "%s: block_size %d must be a power of two <= 1024", who, block_size);
+  if (pool_dtype == HPA_I8 && (!k_scale || !v_scale))
+    return fail(HPA_ERR_ARG, "%s: int8 pool needs k_scale and v_scale", who);
+  if (pool_dtype != HPA_I8 && (pool_dtype < HPA_F32 || pool_dtype > HPA_BF16))
+    return fail(HPA_ERR_UNSUPPORTED, "%s: pool dtype %d", who, pool_dtype);
+  WriteArgs a{k, v, k_pool, v_pool, k_scale, v_scale, block_tables, table_stride, cu_tokens,
+              start_positions, num_kv_heads, head_dim, bsl, num_blocks, rope_cos,
+              rope_cos ? rope_sin : nullptr, rope_cos ? rope_rows : 0};
+  switch (in_dtype) {
+    case HPA_F32: return launch_write_input<F32>(a, pool_dtype, scale_dtype, num_seqs, max_tokens, stream);
+    case HPA_F16: return launch_write_input<F16>(a, pool_dtype, scale_dtype, num_seqs, max_tokens, stream);
+    case HPA_BF16: return launch_write_input<BF16>(a, pool_dtype, scale_dtype, num_seqs, max_tokens, stream);
+  }
+  return fail(HPA_ERR_UNSUPPORTED, "%s: input dtype %d", who, in_dtype);
+}
+
 extern "C" int hpa_kv_write(const void* k, const void* v, int in_dtype, void* k_pool, void* v_pool,
                             int pool_dtype, void* k_scale, void* v_scale, int scale_dtype,
                             const int32_t* block_tables, int table_stride,
                             const int32_t* cu_tokens, const int32_t* start_positions, int num_seqs,
                             int max_tokens, int num_kv_heads, int head_dim, int block_size,
                             int num_blocks, hipStream_t stream) {
-  if (num_seqs == 0 || max_tokens == 0) return HPA_OK;
-  if (!k || !v || !k_pool || !v_pool || !block_tables || !cu_tokens || !start_positions)
-    return fail(HPA_ERR_ARG, "hpa_kv_write: null pointer argument");
-  if (num_seqs < 0 || max_tokens < 0 || num_kv_heads <= 0 || head_dim <= 0 || table_stride <= 0 ||
-      num_blocks <= 0)
-    return fail(HPA_ERR_ARG, "hpa_kv_write: bad shape");
-  const int bsl = ilog2_exact(block_size);
-  if (bsl < 0 || bsl > 10)
-    return fail(HPA_ERR_UNSUPPORTED, "hpa_kv_write: block_size %d must be a power of two <= 1024",
-                block_size);
-  if (pool_dtype == HPA_I8 && (!k_scale || !v_scale))
-    return fail(HPA_ERR_ARG, "hpa_kv_write: int8 pool needs k_scale and v_scale");
-  if (pool_dtype != HPA_I8 && (pool_dtype < HPA_F32 || pool_dtype > HPA_BF16))
-    return fail(HPA_ERR_UNSUPPORTED, "hpa_kv_write: pool dtype %d", pool_dtype);
-  WriteArgs a{k, v, k_pool, v_pool, k_scale, v_scale, block_tables, table_stride, cu_tokens,
-              start_positions, num_kv_heads, head_dim, bsl, num_blocks};
-  switch (in_dtype) {
-    case HPA_F32: return launch_write_input<F32>(a, pool_dtype, scale_dtype, num_seqs, max_tokens, stream);
-    case HPA_F16: return launch_write_input<F16>(a, pool_dtype, scale_dtype, num_seqs, max_tokens, stream);
-    case HPA_BF16: return launch_write_input<BF16>(a, pool_dtype, scale_dtype, num_seqs, max_tokens, stream);
-  }
-  return fail(HPA_ERR_UNSUPPORTED, "hpa_kv_write: input dtype %d", in_dtype);
+  return kv_write_impl("hpa_kv_write", k, v, in_dtype, k_pool, v_pool, pool_dtype, k_scale, v_scale,
+                       scale_dtype, block_tables, table_stride, cu_tokens, start_positions, num_seqs,
+                       max_tokens, num_kv_heads, head_dim, block_size, num_blocks, nullptr, nullptr, 0,
+                       stream);
+}
+
+extern "C" int hpa_kv_write_rope(const void* k, const void* v, int in_dtype, void* k_pool, void* v_pool,
+                                 int pool_dtype, void* k_scale, void* v_scale, int scale_dtype,
+                                 const int32_t* block_tables, int table_stride,
+                                 const int32_t* cu_tokens, const int32_t* start_positions, int num_seqs,
+                                 int max_tokens, int num_kv_heads, int head_dim, int block_size,
+                                 int num_blocks, const float* rope_cos, const float* rope_sin,
+                                 int rope_rows, hipStream_t stream) {
+  if (!rope_cos || !rope_sin) return fail(HPA_ERR_ARG, "hpa_kv_write_rope: null rotary table");
+  return kv_write_impl("hpa_kv_write_rope", k, v, in_dtype, k_pool, v_pool, pool_dtype, k_scale, v_scale,
+                       scale_dtype, block_tables, table_stride, cu_tokens, start_positions, num_seqs,
+                       max_tokens, num_kv_heads, head_dim, block_size, num_blocks, rope_cos, rope_sin,
+                       rope_rows, stream);
 }
 
 extern "C" int hpa_kv_gather(const void* k_pool, const void* v_pool, int pool_dtype,

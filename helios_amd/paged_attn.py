@@ -213,9 +213,15 @@ def write_kv(
     query_lens: Optional[LensArg] = None,
     cu_query_lens: Optional[torch.Tensor] = None,
     max_query_len: Optional[int] = None,
+    rope: Optional[Tuple[torch.Tensor, torch.Tensor]] = None,
 ) -> None:
     """Scatter (fp) or quantize-and-scatter (int8) K/V of a ragged batch in
-    one launch.  k, v: [sum(query_lens), n_kv_heads, head_dim]; sequence b's
+    one launch.  With rope=(cos, sin) -- fp32 [max_positions, head_dim / 2]
+    device tables, as helios' build_rope_cache makes them (model.py:117-132)
+    -- K is rotated rotate-half style by each token's position on the way in
+    (apply_rope, model.py:135-153, fused into the write) and V is written as
+    is; positions without a table row are skipped like positions without a
+    block.  k, v: [sum(query_lens), n_kv_heads, head_dim]; sequence b's
     tokens go to positions start_positions[b].. through block_tables[b].
     With one sequence and no query_lens, every token belongs to it.  A caller
     that keeps int32 device metadata passes cu_query_lens ([n + 1] offsets)
@@ -250,15 +256,26 @@ def write_kv(
     k = k.contiguous()
     v = v.contiguous()
     ks, vs = kv_cache._scales()
-    st = lib().hpa_kv_write(
+    args = (
         ptr(k), ptr(v), DTYPE_CODE[k.dtype], ptr(kv_cache.k_cache), ptr(kv_cache.v_cache),
         DTYPE_CODE[kv_cache.pool_dtype], ptr(ks), ptr(vs),
         DTYPE_CODE[ks.dtype] if ks is not None else 0, ptr(tables), tables.shape[1],
         ptr(cu_t), ptr(starts), n_seqs, max_q,
         kv_cache.n_kv_heads, kv_cache.head_dim, kv_cache.block_size, kv_cache.num_blocks,
-        stream_ptr(dev),
     )
-    check(st, "hpa_kv_write")
+    if rope is None:
+        check(lib().hpa_kv_write(*args, stream_ptr(dev)), "hpa_kv_write")
+        return
+    cos, sin = rope
+    half = kv_cache.head_dim // 2
+    for t, name in ((cos, "cos"), (sin, "sin")):
+        _require_gpu(t, f"the rope {name} table")
+        if t.dtype != torch.float32 or t.dim() != 2 or t.shape[1] != half or not t.is_contiguous():
+            raise ValueError(f"rope {name} must be a contiguous float32 [rows, {half}] tensor")
+    if cos.shape != sin.shape:
+        raise ValueError("rope cos and sin tables differ in shape")
+    check(lib().hpa_kv_write_rope(*args, ptr(cos), ptr(sin), cos.shape[0], stream_ptr(dev)),
+          "hpa_kv_write_rope")
 
 
 def copy_blocks(caches: Sequence[PagedKVCache], pairs: Sequence[Tuple[int, int]]) -> None:

@@ -128,6 +128,24 @@ int hpa_kv_write(const void* k, const void* v, int in_dtype, void* k_pool, void*
                  const int32_t* start_positions, int num_seqs, int max_tokens, int num_kv_heads,
                  int head_dim, int block_size, int num_blocks, hipStream_t stream);
 
+/* hpa_kv_write with K rotated rotate-half style (RoPE) by its write position
+ * on the way into the pool: the step before attention fused into the write,
+ * so K is written once, rotated (and, for int8 pools, quantized from the
+ * rotated values).  rope_cos / rope_sin are fp32 [rope_rows][head_dim / 2]
+ * tables, as helios' build_rope_cache makes them; with c, s = row pos, element
+ * j < head_dim/2 becomes x[j] c[j] - x[j + head_dim/2] s[j] and element
+ * j + head_dim/2 becomes x[j + head_dim/2] c[j] + x[j] s[j], every product and
+ * sum rounded to fp32.  V is written as is.  Positions at or past rope_rows
+ * are skipped, like positions without a block.  head_dim must be even.
+ * Replaces apply_rope on K followed by the cache write (exec/model.py:135-153,
+ * :196-206, :236-247). */
+int hpa_kv_write_rope(const void* k, const void* v, int in_dtype, void* k_pool, void* v_pool,
+                      int pool_dtype, void* k_scale, void* v_scale, int scale_dtype,
+                      const int32_t* block_tables, int table_stride, const int32_t* cu_tokens,
+                      const int32_t* start_positions, int num_seqs, int max_tokens, int num_kv_heads,
+                      int head_dim, int block_size, int num_blocks, const float* rope_cos,
+                      const float* rope_sin, int rope_rows, hipStream_t stream);
+
 /* Gather one sequence's first context_len positions into contiguous
  * [context_len, num_kv_heads, head_dim] tensors of out_dtype; int8 pools are
  * dequantised as fp32(q) * fp32(scale) then rounded.

@@ -12,6 +12,9 @@ each one is pinned (tests/test_oracle.py):
                            clamp and zero-row cases, an independent float64
                            division, and the round-trip bound of the
                            reference's tests/quant/test_kv_quant.py:61-90
+  apply_rope               position 0 is the identity, exact hand-computed
+                           rotations, and bit-equality with torch's CPU
+                           elementwise ops evaluating helios' expression
   PagedPool.write/gather   closed-form position -> (block, offset) mapping,
                            scattered-block round trips and the IndexError
                            texts of tests/parity/test_parity.py:134-148 and
@@ -72,6 +75,31 @@ def dequantize(q: np.ndarray, s_stored: np.ndarray, out_dtype=np.float32) -> np.
 
 
 # ------------------------------------------------------------------ KV pool
+
+
+# ------------------------------------------------------------------ rotary
+
+
+def build_rope_cache(max_pos: int, head_dim: int, theta: float = 10000.0) -> Tuple[np.ndarray, np.ndarray]:
+    """exec/model.py:117-132: inv_freq = 1 / theta^(2i/d), cos and sin of
+    pos x inv_freq, [max_pos, head_dim / 2] float32.  (Tests that need
+    helios' exact tables build them with torch; callers pass tables in.)"""
+    inv = (1.0 / (np.float32(theta) ** (np.arange(0, head_dim, 2, dtype=np.float32) / np.float32(head_dim))))
+    freqs = np.outer(np.arange(max_pos, dtype=np.float32), inv.astype(np.float32)).astype(np.float32)
+    return np.cos(freqs).astype(np.float32), np.sin(freqs).astype(np.float32)
+
+
+def apply_rope(x: np.ndarray, cos: np.ndarray, sin: np.ndarray, positions: np.ndarray) -> np.ndarray:
+    """exec/model.py:135-153, rotate-half: x [n, heads, d] (promoted to
+    float32), c, s = cos/sin[positions]; (x1 c - x2 s, x2 c + x1 s).  Every
+    product and sum is a separate float32 operation, rounded on its own, as
+    torch's elementwise ops round them."""
+    x = np.asarray(x, dtype=np.float32)
+    c = np.asarray(cos, np.float32)[positions][:, None, :]
+    s = np.asarray(sin, np.float32)[positions][:, None, :]
+    half = x.shape[-1] // 2
+    x1, x2 = x[..., :half], x[..., half:]
+    return np.concatenate((x1 * c - x2 * s, x2 * c + x1 * s), axis=-1).astype(np.float32)
 
 
 class PagedPool:

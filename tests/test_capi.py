@@ -31,7 +31,8 @@ def lib():
 def test_header_declares_the_expected_entry_points():
     assert _declared() == sorted([
         "hpa_version", "hpa_last_error", "hpa_decode_workspace_size", "hpa_paged_decode",
-        "hpa_paged_prefill", "hpa_kv_write", "hpa_kv_gather", "hpa_copy_blocks",
+        "hpa_paged_prefill", "hpa_kv_write", "hpa_kv_write_rope", "hpa_kv_gather",
+        "hpa_copy_blocks",
     ])
 
 
@@ -103,6 +104,13 @@ def test_argument_errors_return_status_without_a_gpu(lib):
     st = lib.hpa_kv_write(dummy, dummy, 1, dummy, dummy, 3, None, None, 1, dummy, 1, dummy, dummy,
                           1, 1, 2, 64, 16, 8, None)
     assert st == _lib.HPA_ERR_ARG
+    # rotary write: missing sin table, odd head_dim
+    st = lib.hpa_kv_write_rope(dummy, dummy, 1, dummy, dummy, 1, None, None, 0, dummy, 1, dummy, dummy,
+                               1, 1, 2, 64, 16, 8, dummy, None, 16, None)
+    assert st == _lib.HPA_ERR_ARG and b"rotary" in lib.hpa_last_error()
+    st = lib.hpa_kv_write_rope(dummy, dummy, 1, dummy, dummy, 1, None, None, 0, dummy, 1, dummy, dummy,
+                               1, 1, 2, 63, 16, 8, dummy, dummy, 16, None)
+    assert st == _lib.HPA_ERR_ARG and b"even head_dim" in lib.hpa_last_error()
     # empty batches are no-ops
     assert lib.hpa_paged_prefill(None, None, 0, None, None, 0, None, None, 0, None, 1, None, None,
                                  None, 0, 0, 1, 1, 64, 16, 1, 1.0, None) == _lib.HPA_OK

@@ -169,3 +169,76 @@ def test_copy_blocks_all_layers_one_launch():
             kk[d] = kk[s]
             vv[d] = vv[s]
         assert torch.equal(c.k_cache, kk) and torch.equal(c.v_cache, vv)
+
+
+def _rope_tables(max_pos, d, theta=10000.0):
+    """helios' build_rope_cache (exec/model.py:117-132), evaluated by torch."""
+    inv = 1.0 / (theta ** (torch.arange(0, d, 2, dtype=torch.float32) / d))
+    freqs = torch.outer(torch.arange(max_pos, dtype=torch.float32), inv)
+    return freqs.cos(), freqs.sin()
+
+
+@pytest.mark.parametrize("scale_dtype", [torch.float16, torch.float32])
+def test_rope_fused_int8_write_is_bit_exact(scale_dtype):
+    """K rotated by its position and quantized in one pass equals helios'
+    apply_rope followed by the quantizing write, bit for bit; V untouched."""
+    gen = torch.Generator().manual_seed(7)
+    H, D, bs, nb = 8, 128, 16, 64
+    qlens, starts = [5, 19, 1], [0, 30, 200]
+    perm = np.random.default_rng(7).permutation(nb)
+    tables = [[int(x) for x in perm[16 * i:16 * i + 16]] for i in range(3)]
+    cos, sin = _rope_tables(512, D)
+    k = (torch.randn(sum(qlens), H, D, generator=gen) * 2).half()
+    v = torch.randn(sum(qlens), H, D, generator=gen).half()
+    cache = QuantizedPagedKVCache(nb, bs, H, D, dtype=torch.float16, device="cuda", scale_dtype=scale_dtype)
+    write_kv(cache, tables, starts, k.cuda(), v.cuda(), query_lens=qlens, rope=(cos.cuda(), sin.cuda()))
+    pool = R.PagedPool(nb, bs, H, D, np.float32, quantized=True,
+                       scale_dtype=np.float16 if scale_dtype == torch.float16 else np.float32)
+    lo = 0
+    for t, n, s0 in zip(tables, qlens, starts):
+        pos = np.arange(s0, s0 + n)
+        kr = R.apply_rope(k[lo:lo + n].numpy(), cos.numpy(), sin.numpy(), pos)
+        pool.write(t, s0, kr, v[lo:lo + n].float().numpy())
+        lo += n
+    torch.cuda.synchronize()
+    assert np.array_equal(to_np(cache.k_cache), pool.k)
+    assert np.array_equal(to_np(cache.k_scale), pool.k_scale)
+    assert np.array_equal(to_np(cache.v_cache), pool.v)
+    assert np.array_equal(to_np(cache.v_scale), pool.v_scale)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_rope_fused_fp_write_matches_oracle(dtype):
+    gen = torch.Generator().manual_seed(8)
+    H, D, bs, nb = 2, 64, 16, 16
+    qlens, starts = [17, 3], [5, 60]
+    tables = [[3, 9, 1], [7, 2, 11, 4, 0]]
+    cos, sin = _rope_tables(128, D)
+    k = torch.randn(sum(qlens), H, D, generator=gen).to(dtype)
+    v = torch.randn(sum(qlens), H, D, generator=gen).to(dtype)
+    cache = PagedKVCache(nb, bs, H, D, dtype=dtype, device="cuda")
+    write_kv(cache, tables, starts, k.cuda(), v.cuda(), query_lens=qlens, rope=(cos.cuda(), sin.cuda()))
+    lo = 0
+    got_k, got_v = cache.k_cache.cpu(), cache.v_cache.cpu()
+    for t, n, s0 in zip(tables, qlens, starts):
+        kr = torch.from_numpy(R.apply_rope(k[lo:lo + n].float().numpy(), cos.numpy(), sin.numpy(),
+                                           np.arange(s0, s0 + n))).to(dtype)
+        for i in range(n):
+            p = s0 + i
+            blk, off = t[p // bs], p % bs
+            assert torch.equal(got_k[blk, :, off, :], kr[i])
+            assert torch.equal(got_v[blk, :, off, :], v[lo + i])
+        lo += n
+
+
+def test_rope_positions_past_the_table_are_skipped():
+    H, D, bs = 1, 32, 16
+    cos, sin = _rope_tables(20, D)            # rows for positions 0..19 only
+    cache = PagedKVCache(4, bs, H, D, dtype=torch.float32, device="cuda")
+    k = torch.ones(6, H, D, device="cuda")
+    write_kv(cache, [[0, 1]], [16], k, k, rope=(cos.cuda(), sin.cuda()))   # positions 16..21
+    got = cache.k_cache.cpu()
+    assert torch.count_nonzero(got[1, 0, :4]) == 4 * D       # positions 16..19 written
+    assert torch.count_nonzero(got[1, 0, 4:6]) == 0          # 20, 21 have no table row
+    with pytest.raises(ValueError):
+        write_kv(cache, [[0, 1]], [0], k, k, rope=(cos.cuda(), sin.cuda()[:, :3]))

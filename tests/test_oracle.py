@@ -295,3 +295,68 @@ def test_tie_vectors_catch_round_half_away():
     away = np.sign(x / s) * np.floor(np.abs(x / s) + 0.5)
     q, _ = R.quantize(x)
     assert not np.array_equal(away.astype(np.int8), q)
+
+
+# ------------------------------------------------------------------ rotary
+
+def _helios_rope_tables(max_pos, d, theta=10000.0):
+    """helios' own table recipe (exec/model.py:117-132), evaluated by torch."""
+    import torch
+
+    inv = 1.0 / (theta ** (torch.arange(0, d, 2, dtype=torch.float32) / d))
+    freqs = torch.outer(torch.arange(max_pos, dtype=torch.float32), inv)
+    return freqs.cos().numpy(), freqs.sin().numpy()
+
+
+def test_rope_position_zero_is_identity():
+    cos, sin = _helios_rope_tables(8, 16)
+    x = np.random.default_rng(0).standard_normal((3, 2, 16)).astype(np.float32)
+    out = R.apply_rope(x, cos, sin, np.zeros(3, dtype=np.int64))
+    assert np.array_equal(out, x)
+
+
+def test_rope_hand_computed_rotation():
+    # c = 0.5, s = 0.75 are exact in binary, so every product and sum is exact
+    cos = np.array([[1.0, 1.0], [0.5, 0.5]], np.float32)
+    sin = np.array([[0.0, 0.0], [0.75, 0.75]], np.float32)
+    x = np.array([[[1.0, -2.0, 2.0, 4.0]]], np.float32)   # x1 = (1, -2), x2 = (2, 4)
+    out = R.apply_rope(x, cos, sin, np.array([1]))
+    # (x1 c - x2 s, x2 c + x1 s)
+    assert out.tolist() == [[[0.5 - 1.5, -1.0 - 3.0, 1.0 + 0.75, 2.0 - 1.5]]]
+
+
+def test_rope_matches_torch_elementwise_bit_for_bit():
+    """helios evaluates x1 * c - x2 * s with torch elementwise ops on fp16 or
+    fp32 inputs promoted to fp32; the oracle's float32 NumPy ops round the
+    same way, so the rotated values (and everything quantized from them)
+    agree bit for bit."""
+    import torch
+
+    cos, sin = _helios_rope_tables(512, 128)
+    rng = np.random.default_rng(1)
+    for dt in (np.float16, np.float32):
+        x = (rng.standard_normal((40, 8, 128)) * 3).astype(dt)
+        pos = rng.integers(0, 512, size=40)
+        xt = torch.from_numpy(x)
+        c = torch.from_numpy(cos)[torch.from_numpy(pos)].unsqueeze(1)
+        s = torch.from_numpy(sin)[torch.from_numpy(pos)].unsqueeze(1)
+        x1, x2 = xt.chunk(2, dim=-1)
+        want = torch.cat((x1 * c - x2 * s, x2 * c + x1 * s), dim=-1).numpy()
+        got = R.apply_rope(x, cos, sin, pos)
+        assert got.dtype == np.float32 and np.array_equal(got, want)
+
+
+def test_rope_planted_sign_mistake_is_caught():
+    cos = np.array([[0.5, 0.5]], np.float32)
+    sin = np.array([[0.75, 0.75]], np.float32)
+    x = np.array([[[1.0, -2.0, 2.0, 4.0]]], np.float32)
+    good = R.apply_rope(x, cos, sin, np.array([0]))
+    x1, x2 = x[..., :2], x[..., 2:]
+    wrong = np.concatenate((x1 * 0.5 + x2 * 0.75, x2 * 0.5 - x1 * 0.75), axis=-1)
+    assert not np.array_equal(good, wrong)
+
+
+def test_rope_table_restatement_close_to_helios():
+    cos, sin = _helios_rope_tables(256, 64)
+    c2, s2 = R.build_rope_cache(256, 64)
+    assert np.abs(cos - c2).max() < 1e-4 and np.abs(sin - s2).max() < 1e-4

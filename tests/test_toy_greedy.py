@@ -117,3 +117,29 @@ def test_toy_greedy_with_hip_attention_matches_helios(golden, weights):
             toks = greedy(model, attn, case["prompt"], case["n_new"], table)
         torch.cuda.synchronize()
         assert toks == case["tokens"], f"case {i}"
+
+
+class HipAttentionFusedRope(HipAttention):
+    """K rotated inside the cache write (write_kv with the model's tables)."""
+
+    fused_rope = True
+
+    def __init__(self, n_kv_heads, head_dim, cos, sin):
+        super().__init__(n_kv_heads, head_dim)
+        self.cos, self.sin = cos.contiguous(), sin.contiguous()
+
+    def write(self, cache, block_ids, start_pos, k, v):
+        self.H.write_kv(cache, [list(block_ids)], [start_pos], k, v, rope=(self.cos, self.sin))
+
+
+@pytest.mark.gpu
+def test_toy_greedy_with_fused_rope_write_matches_helios(golden, weights):
+    model = ToyModel(weights, "cuda")
+    attn = HipAttentionFusedRope(TOY["num_key_value_heads"], model.hd, model.cos, model.sin)
+    for i, case in enumerate(golden["cases"]):
+        print(f"toy greedy (fused rope write) case {i}", flush=True)
+        table = _table(len(case["prompt"]) + case["n_new"], seed=20 + i)
+        with torch.inference_mode():
+            toks = greedy(model, attn, case["prompt"], case["n_new"], table)
+        torch.cuda.synchronize()
+        assert toks == case["tokens"], f"case {i}"

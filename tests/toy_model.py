@@ -131,7 +131,11 @@ class ToyModel:
             q = (x @ W[pre + "self_attn.q_proj.weight"].T).view(n, self.nq, self.hd)
             k = (x @ W[pre + "self_attn.k_proj.weight"].T).view(n, self.nkv, self.hd)
             v = (x @ W[pre + "self_attn.v_proj.weight"].T).view(n, self.nkv, self.hd)
-            q, k = self._rope(q, pos), self._rope(k, pos)
+            q = self._rope(q, pos)
+            # a backend that fuses the rotation into its K write gets K as
+            # projected, plus the model's rotary tables
+            if not getattr(attn, "fused_rope", False):
+                k = self._rope(k, pos)
             start = positions[0]
             attn.write(cache, block_ids, start, k, v)
             if is_decode:
