@@ -319,6 +319,100 @@ def _traffic(workload_key):
         return json.load(f).get("bytes_per_launch")
 
 
+def meta_bench(device, layers, steps, warmup, seed=4):
+    """Wall time of one decode-verify step of config 5's batch over ``layers``
+    layers, with the step's attention metadata (a) handed to every layer's
+    call as the runner's Python lists (helios' pattern: exec/runner.py:261-268
+    builds them, each layer's call converts them, triton_attn.py:156-165) and
+    (b) prepared once per step in device-resident tables (DeviceBlockTables)
+    and passed to every layer as device tensors.  Contexts grow by one token
+    per step; a table gains a block when its context crosses a block
+    boundary.  One pool serves every layer (the per-layer kernels are the
+    same; only the metadata path differs)."""
+    import numpy as np
+    import torch
+
+    import helios_amd as H
+
+    wl = DecodeWorkload(5, device, seed)
+    rng = np.random.default_rng(seed + 1)
+    cache = wl.caches[0]
+    nb = cache.num_blocks
+    tables = [[int(x) for x in row[: (c + BLOCK - 1) // BLOCK]] for row, c in zip(wl.tables_np, wl.lens)]
+    lens = list(wl.lens)
+    Tq = wl.Tq
+    width = max(len(t) for t in tables) + (steps + warmup + 10) // BLOCK + 2
+    tabs = H.DeviceBlockTables.for_cache(cache, wl.B, width)
+    q = wl.q
+
+    def advance():
+        for i in range(len(lens)):
+            lens[i] += 1
+            if (lens[i] + BLOCK - 1) // BLOCK > len(tables[i]):
+                tables[i].append(int(rng.integers(nb)))
+
+    def step_lists():
+        advance()
+        for _ in range(layers):
+            H.paged_attention_verify_batched(q, cache, tables, lens, Tq, wl.scale)
+
+    prep = []
+
+    def step_device():
+        advance()
+        t0 = time.perf_counter()
+        meta = tabs.prepare(range(len(lens)), tables, lens, [c - Tq for c in lens], [Tq] * len(lens), True)
+        prep.append(time.perf_counter() - t0)
+        for _ in range(layers):
+            H.batched_attention(q, cache, meta, wl.scale)
+
+    res = {}
+    for name, fn in (("lists", step_lists), ("device", step_device)):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        prep.clear()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        ev0.record()
+        for _ in range(steps):
+            fn()
+        ev1.record()
+        torch.cuda.synchronize()
+        res[name] = ((time.perf_counter() - t0) * 1e3 / steps, ev0.elapsed_time(ev1) / steps)
+        print(f"{name}: {res[name][0]:.3f} ms/step wall", file=sys.stderr, flush=True)
+    # prepare's own host cost, with the GPU idle (in the loop above it also
+    # waits whenever the host runs two steps ahead of the GPU)
+    idle = []
+    for _ in range(10):
+        advance()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        meta = tabs.prepare(range(len(lens)), tables, lens, [c - Tq for c in lens], [Tq] * len(lens), True)
+        idle.append(time.perf_counter() - t0)
+    torch.cuda.synchronize()
+    # the layers' kernels alone, metadata already on the device
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(steps):
+        for _ in range(layers):
+            H.batched_attention(q, cache, meta, wl.scale)
+    ev1.record()
+    torch.cuda.synchronize()
+    kernels_ms = ev0.elapsed_time(ev1) / steps
+    print(json.dumps({
+        "metric": f"decode-verify step wall time over {layers} layers (config 5 batch): "
+                  "device-resident step metadata vs per-layer Python lists",
+        "value": round(res["device"][0], 3), "unit": "ms/step", "higher_is_better": False,
+        "lists_ms_per_step": round(res["lists"][0], 3),
+        "kernels_only_ms_per_step": round(kernels_ms, 3),
+        "prepare_us_median_in_loop": round(float(np.median(prep)) * 1e6, 1),
+        "prepare_us_median_gpu_idle": round(float(np.median(idle)) * 1e6, 1),
+        "steps": steps, "warmup": warmup, "layers": layers,
+        "config": {"workload": wl.name, "batch": wl.B, "q_per_seq": Tq},
+    }))
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -334,6 +428,9 @@ def main():
                     help="pool copies rotated per step (default: enough to exceed 256 MB)")
     ap.add_argument("--cpu-budget", type=float, default=15.0,
                     help="seconds of CPU baseline work (0 disables it)")
+    ap.add_argument("--meta-layers", type=int, default=0, metavar="L",
+                    help="only time a decode-verify step over L layers with device-resident "
+                         "vs per-layer list metadata, print its own JSON line, and exit")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run 5 plain device copies of MIB MiB (the known-size kernel "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings) and exit")
@@ -365,6 +462,9 @@ def main():
     if not torch.cuda.is_available():
         raise SystemExit("bench.py needs a GPU")
     device = torch.device("cuda:0")
+    if args.meta_layers:
+        meta_bench(device, args.meta_layers, min(args.steps, 20), min(args.warmup, 5))
+        return
     seed = args.config - 1 if args.seed is None else args.seed
 
     if args.config == 4:

@@ -23,6 +23,7 @@ from .paged_attn import (  # noqa: F401
     paged_attention_verify_batched,
     write_kv,
 )
+from .step_meta import DeviceAttnMeta, DeviceBlockTables, batched_attention, write_kv_batched  # noqa: F401
 
 __all__ = [
     "PagedKVCache",
@@ -37,4 +38,8 @@ __all__ = [
     "paged_attention_varlen",
     "paged_attention_verify_batched",
     "write_kv",
+    "DeviceAttnMeta",
+    "DeviceBlockTables",
+    "batched_attention",
+    "write_kv_batched",
 ]

@@ -80,6 +80,10 @@ SIGNATURES = {
         [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr, _c_int, _c_int, _c_size,
          _c_size, _c_ptr],
     ),
+    "hpa_step_tables": (
+        _c_int,
+        [_c_ptr, _c_int, _c_ptr, _c_int, _c_ptr, _c_int, _c_int, _c_ptr, _c_int, _c_ptr],
+    ),
 }
 
 _lib: Optional[ctypes.CDLL] = None

@@ -173,6 +173,27 @@ int hpa_copy_blocks(void* const* k_pools, void* const* v_pools, void* const* k_s
                     int num_blocks, size_t block_bytes, size_t scale_block_bytes,
                     hipStream_t stream);
 
+/* One step's block tables from tables kept in device memory across steps.
+ * Replaces rebuilding every table from Python lists each step
+ * (reference exec/runner.py:205-225, 263-268) and converting them to device
+ * tensors in every attention call of every layer (exec/triton_attn.py:156-165,
+ * paged_attn.py:106, 347-348).
+ *   resident       device int32 [resident_rows][resident_width]: one row per
+ *                  resident sequence, updated in place
+ *   entries        device int32 [num_entries][5] = (row, n_blocks, upd_first,
+ *                  upd_count, upd_offset), one per sequence of the step, in
+ *                  batch order; rows must be distinct within a call
+ *   new_ids        device int32 [num_new_ids]: entry e's replaced table
+ *                  entries upd_first .. upd_first + upd_count - 1 are
+ *                  new_ids[upd_offset ..]
+ *   step_tables    device int32 [num_entries][step_width], written: entry e's
+ *                  row after the update, entries >= n_blocks as 0 (the
+ *                  zero-padded table of triton_attn.py:156-165)
+ * Rows outside [0, resident_rows) give all-zero step rows. */
+int hpa_step_tables(const int32_t* entries, int num_entries, const int32_t* new_ids,
+                    int num_new_ids, int32_t* resident, int resident_rows, int resident_width,
+                    int32_t* step_tables, int step_width, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

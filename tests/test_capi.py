@@ -32,7 +32,7 @@ def test_header_declares_the_expected_entry_points():
     assert _declared() == sorted([
         "hpa_version", "hpa_last_error", "hpa_decode_workspace_size", "hpa_paged_decode",
         "hpa_paged_prefill", "hpa_kv_write", "hpa_kv_write_rope", "hpa_kv_gather",
-        "hpa_copy_blocks",
+        "hpa_copy_blocks", "hpa_step_tables",
     ])
 
 
@@ -111,6 +111,12 @@ def test_argument_errors_return_status_without_a_gpu(lib):
     st = lib.hpa_kv_write_rope(dummy, dummy, 1, dummy, dummy, 1, None, None, 0, dummy, 1, dummy, dummy,
                                1, 1, 2, 63, 16, 8, dummy, dummy, 16, None)
     assert st == _lib.HPA_ERR_ARG and b"even head_dim" in lib.hpa_last_error()
+    # step tables: wider than the resident rows, null resident array
+    st = lib.hpa_step_tables(dummy, 1, None, 0, dummy, 4, 8, dummy, 9, None)
+    assert st == _lib.HPA_ERR_ARG and b"step width 9" in lib.hpa_last_error()
+    st = lib.hpa_step_tables(dummy, 1, None, 0, None, 4, 8, dummy, 8, None)
+    assert st == _lib.HPA_ERR_ARG and b"null pointer" in lib.hpa_last_error()
+    assert lib.hpa_step_tables(None, 0, None, 0, None, 0, 0, None, 0, None) == _lib.HPA_OK
     # empty batches are no-ops
     assert lib.hpa_paged_prefill(None, None, 0, None, None, 0, None, None, 0, None, 1, None, None,
                                  None, 0, 0, 1, 1, 64, 16, 1, 1.0, None) == _lib.HPA_OK
