@@ -413,6 +413,91 @@ def meta_bench(device, layers, steps, warmup, seed=4):
     }))
 
 
+def spec_bench(device, gamma, steps, warmup, seed=4):
+    """Attention work of one speculative step for config 5's batch, one
+    layer: gamma draft decodes over an int8 KV shadow (each writing its
+    token), the verify pass (gamma tokens per sequence written to and
+    attended over the int8 target cache) and the shadow's re-sync (gamma
+    tokens written and attended).  Batched: 2 gamma + 4 launches for the
+    whole batch (DeviceAttnMeta.advanced / .verify).  Per sequence, as
+    helios runs speculation (exec/runner.py:131-133, :302-406): the same
+    calls once per sequence."""
+    import numpy as np
+    import torch
+
+    import helios_amd as H
+
+    wl = DecodeWorkload(5, device, seed)
+    target = wl.caches[0]
+    shadow = H.QuantizedPagedKVCache(target.num_blocks, BLOCK, wl.Hkv, wl.D, dtype=torch.float16,
+                                     device=device, scale_dtype=torch.float16)
+    for a, b in ((shadow.k_cache, target.k_cache), (shadow.v_cache, target.v_cache),
+                 (shadow.k_scale, target.k_scale), (shadow.v_scale, target.v_scale)):
+        a.copy_(b)
+    B, Hq, Hkv, D = wl.B, wl.Hq, wl.Hkv, wl.D
+    # contexts leave room for the gamma speculative positions inside the last block
+    lens = [max(1, c - gamma) for c in wl.lens]
+    tables = [[int(x) for x in row[: (c + BLOCK - 1) // BLOCK]] for row, c in zip(wl.tables_np, wl.lens)]
+    tabs = H.DeviceBlockTables.for_cache(target, B, max(len(t) for t in tables))
+    gen = torch.Generator(device=device).manual_seed(seed)
+    q1 = torch.randn(B, Hq, D, generator=gen, device=device, dtype=torch.float16)
+    k1 = torch.randn(B, Hkv, D, generator=gen, device=device, dtype=torch.float16)
+    qg = torch.randn(B * gamma, Hq, D, generator=gen, device=device, dtype=torch.float16)
+    kg = torch.randn(B * gamma, Hkv, D, generator=gen, device=device, dtype=torch.float16)
+    base = tabs.prepare(range(B), tables, lens, [c - 1 for c in lens], [1] * B, True)
+    drafts = [base.advanced(j) for j in range(gamma)]
+    vm = base.verify(gamma)
+    sc = wl.scale
+
+    def batched():
+        for m in drafts:
+            H.write_kv_batched(shadow, m, k1, k1)
+            H.batched_attention(q1, shadow, m, sc)
+        H.write_kv_batched(target, vm, kg, kg)
+        H.batched_attention(qg, target, vm, sc)
+        H.write_kv_batched(shadow, vm, kg, kg)
+        H.batched_attention(qg, shadow, vm, sc)
+
+    def per_sequence():
+        for b in range(B):
+            t, c = tables[b], lens[b]
+            for j in range(gamma):
+                shadow.write(t, c - 1 + j, k1[b:b + 1], k1[b:b + 1])
+                H.paged_attention_decode(q1[b], shadow, t, c + j, sc)
+            qb, kb = qg[b * gamma:(b + 1) * gamma], kg[b * gamma:(b + 1) * gamma]
+            target.write(t, c - 1, kb, kb)
+            H.paged_attention_prefill(qb, target, t, c - 1, c + gamma - 1, sc)
+            shadow.write(t, c - 1, kb, kb)
+            H.paged_attention_prefill(qb, shadow, t, c - 1, c + gamma - 1, sc)
+
+    res = {}
+    for name, fn, n, w in (("batched", batched, steps, warmup), ("per_sequence", per_sequence, 2, 1)):
+        for _ in range(w):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            fn()
+        torch.cuda.synchronize()
+        res[name] = (time.perf_counter() - t0) * 1e3 / n
+        print(f"{name}: {res[name]:.3f} ms per layer-step", file=sys.stderr, flush=True)
+    # K/V bytes read (int8 payload + fp16 scale per token, head and tensor):
+    # draft j attends context + j, verify and re-sync attend context + gamma - 1
+    row = 2 * Hkv * (D + 2)
+    kv_read = sum(lens) * row
+    alg = gamma * kv_read + B * (gamma * (gamma - 1) // 2) * row + 2 * (kv_read + B * (gamma - 1) * row)
+    print(json.dumps({
+        "metric": f"speculative step attention (gamma {gamma}, int8 target + int8 draft shadow, "
+                  "config 5 batch, one layer): batched vs per sequence",
+        "value": round(res["batched"], 3), "unit": "ms per layer-step", "higher_is_better": False,
+        "per_sequence_ms": round(res["per_sequence"], 3),
+        "launches_batched": 2 * (gamma + 2), "launches_per_sequence": 2 * (gamma + 2) * B,
+        "hbm_gbs_batched": round(alg / (res["batched"] * 1e-3) / 1e9, 1),
+        "algorithmic_bytes": int(alg),
+        "config": {"workload": wl.name, "batch": B, "gamma": gamma},
+    }))
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -431,6 +516,9 @@ def main():
     ap.add_argument("--meta-layers", type=int, default=0, metavar="L",
                     help="only time a decode-verify step over L layers with device-resident "
                          "vs per-layer list metadata, print its own JSON line, and exit")
+    ap.add_argument("--spec-gamma", type=int, default=0, metavar="G",
+                    help="only time one speculative step's attention (gamma G, config 5 batch) "
+                         "batched vs per sequence, print its own JSON line, and exit")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run 5 plain device copies of MIB MiB (the known-size kernel "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings) and exit")
@@ -462,6 +550,9 @@ def main():
     if not torch.cuda.is_available():
         raise SystemExit("bench.py needs a GPU")
     device = torch.device("cuda:0")
+    if args.spec_gamma:
+        spec_bench(device, args.spec_gamma, min(args.steps, 50), min(args.warmup, 20))
+        return
     if args.meta_layers:
         meta_bench(device, args.meta_layers, min(args.steps, 20), min(args.warmup, 5))
         return

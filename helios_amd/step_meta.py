@@ -58,6 +58,8 @@ class DeviceAttnMeta:
     max_context_len: int
     max_query_len: int
     is_decode: bool
+    # positions every table can still hold past its context (None: unknown)
+    headroom: Optional[int] = None
 
     @property
     def n_seqs(self) -> int:
@@ -66,6 +68,47 @@ class DeviceAttnMeta:
     @property
     def n_tokens(self) -> int:
         return self.token_slices[-1][1] if self.token_slices else 0
+
+    def _need(self, extra: int) -> None:
+        if extra < 0:
+            raise ValueError("a speculative step cannot go backwards")
+        if self.headroom is not None and extra > self.headroom:
+            raise IndexError(f"a block table holds only {self.headroom} positions past its context; "
+                             f"{extra} needed")
+
+    def advanced(self, j: int) -> "DeviceAttnMeta":
+        """The same one-token decode batch j tokens later -- draft step j of
+        speculative decoding (exec/runner.py:330-346, exec/qassd.py:291-305):
+        every context length and position + j.  Device arithmetic only, no
+        upload and no synchronisation."""
+        if not self.is_decode or self.max_query_len != 1:
+            raise ValueError("advanced() applies to a one-token decode batch")
+        self._need(j)
+        return DeviceAttnMeta(
+            self.token_slices, self.block_tables, self.context_lens + j, self.start_positions + j,
+            self.cu_query_lens, self.query_lens, self.max_context_len + j, 1, True,
+            None if self.headroom is None else self.headroom - j)
+
+    def verify(self, n: int) -> "DeviceAttnMeta":
+        """n query tokens per sequence from each decode position: the verify
+        pass over [last token] + drafted[:-1] at positions position ..
+        position + n - 1, attending context_len + n - 1 keys
+        (exec/runner.py:352-362, exec/qassd.py:309-314).  The same metadata
+        serves the re-sync of the draft's KV shadow (runner.py:397-406)
+        when it is run over all n positions: K/V written past a sequence's
+        committed tokens lie beyond every later draft step's context until
+        that step rewrites them.  Device arithmetic only."""
+        if not self.is_decode or self.max_query_len != 1:
+            raise ValueError("verify() applies to a one-token decode batch")
+        if n < 1:
+            raise ValueError("verify needs at least one token per sequence")
+        self._need(n - 1)
+        b = self.n_seqs
+        cu = torch.arange(0, (b + 1) * n, n, dtype=torch.int32, device=self.context_lens.device)
+        return DeviceAttnMeta(
+            [(i * n, (i + 1) * n) for i in range(b)], self.block_tables, self.context_lens + (n - 1),
+            self.start_positions, cu, [n] * b, self.max_context_len + n - 1, n, True,
+            None if self.headroom is None else self.headroom - (n - 1))
 
 
 @dataclass
@@ -355,6 +398,8 @@ class DeviceBlockTables:
                 max_context_len=max(g.context_lens, default=0),
                 max_query_len=max(g.query_lens, default=0),
                 is_decode=g.is_decode,
+                headroom=(min((len(t) * self.host.block_size - c for t, c in zip(g.tables, g.context_lens)),
+                              default=0) if self.host.block_size else None),
             ))
         return metas
 

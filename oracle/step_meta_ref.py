@@ -9,6 +9,9 @@ the attention calls (reference = anish41338/helios, python/helios/):
   decode_meta    exec/runner.py:250-268  (one token per sequence: context_len
                  and position from the DecodeItem)
   padded_tables  exec/triton_attn.py:156-165 (int32 [n, max len], zero-padded)
+  draft_meta     exec/runner.py:330-346 (draft step j: position and context + j)
+  verify_meta    exec/runner.py:352-362 (n tokens from the decode position,
+                 context_len + n - 1)
 
 Pinned by tests/test_step_meta.py: hand-built steps whose expected metadata
 is written out literally, and the invariants the runner relies on (slices
@@ -92,3 +95,22 @@ def padded_tables(tables: Sequence[Sequence[int]]) -> np.ndarray:
     for i, t in enumerate(tables):
         out[i, : len(t)] = t
     return out
+
+
+def draft_meta(items: Sequence[DecodeItem], j: int) -> Meta:
+    """exec/runner.py:330-346: the draft's j-th forward after the decode
+    item, one token at position + j attending context_len + j keys."""
+    return decode_meta([DecodeItem(it.seq_id, 0, it.position + j, it.block_ids, it.context_len + j)
+                        for it in items])
+
+
+def verify_meta(items: Sequence[DecodeItem], n: int) -> Meta:
+    """exec/runner.py:352-362: verify tokens [last] + drafted[:-1] (n of
+    them) at positions position .. position + n - 1, context_len + n - 1."""
+    return Meta(
+        [(i * n, (i + 1) * n) for i in range(len(items))],
+        [list(it.block_ids) for it in items],
+        [it.context_len + n - 1 for it in items],
+        [it.position for it in items],
+        True,
+    )

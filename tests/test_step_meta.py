@@ -10,7 +10,9 @@ import random
 import numpy as np
 import pytest
 
-from helios_amd.step_meta import TableResidency, make_group, step_groups
+import torch
+
+from helios_amd.step_meta import DeviceAttnMeta, TableResidency, make_group, step_groups
 from oracle import step_meta_ref as M
 
 ENTRY = 5
@@ -237,3 +239,51 @@ def test_lru_reuses_the_oldest_row_not_in_the_step():
     # "b" comes back: its row is re-uploaded from scratch
     plan = res.plan([make_group(["b"], [[2]], [1], [0], [1], True)])
     assert plan.n_new_ids == 1
+
+
+# ------------------------------------------ speculative-step derivations
+
+
+def _host_meta(ref: "M.Meta", headroom=None) -> DeviceAttnMeta:
+    """A DeviceAttnMeta built from the oracle's lists on CPU tensors (the
+    derivations are tensor arithmetic; the device case is tested on the GPU)."""
+    q = [hi - lo for lo, hi in ref.token_slices]
+    cu = [0]
+    for x in q:
+        cu.append(cu[-1] + x)
+    i32 = lambda v: torch.tensor(v, dtype=torch.int32)  # noqa: E731
+    return DeviceAttnMeta(ref.token_slices, torch.from_numpy(M.padded_tables(ref.block_tables)),
+                          i32(ref.context_lens), i32(ref.start_positions), i32(cu), q,
+                          max(ref.context_lens), max(q), ref.is_decode, headroom)
+
+
+def _same(meta: DeviceAttnMeta, ref: "M.Meta"):
+    assert meta.token_slices == ref.token_slices
+    assert meta.context_lens.tolist() == ref.context_lens
+    assert meta.start_positions.tolist() == ref.start_positions
+    cu = meta.cu_query_lens.tolist()
+    assert [(cu[b], cu[b + 1]) for b in range(len(cu) - 1)] == ref.token_slices
+    assert meta.query_lens == [hi - lo for lo, hi in ref.token_slices]
+    assert meta.max_context_len == max(ref.context_lens) and meta.max_query_len == max(meta.query_lens)
+    assert meta.is_decode
+
+
+def test_speculative_metadata_derivations_match_the_runner():
+    items = [M.DecodeItem(0, 5, 16, [3, 4], 17), M.DecodeItem(1, 6, 40, [7, 8, 9, 10], 41),
+             M.DecodeItem(2, 7, 0, [1], 1)]
+    base = _host_meta(M.decode_meta(items), headroom=min(len(i.block_ids) * 16 - i.context_len for i in items))
+    for j in range(4):
+        _same(base.advanced(j), M.draft_meta(items, j))
+    for n in (1, 2, 4):
+        _same(base.verify(n), M.verify_meta(items, n))
+    # hand-checked: verify(3) of the item at position 16 covers positions 16..18
+    v = base.verify(3)
+    assert v.token_slices[0] == (0, 3) and v.context_lens[0] == 19 and v.start_positions[0] == 16
+    # the sequence at context 41 of 64 slots and the one at 1 of 16 leave 15 spare positions
+    assert base.headroom == 15
+    with pytest.raises(IndexError, match="holds only 15 positions"):
+        base.advanced(16)
+    with pytest.raises(IndexError):
+        base.verify(17)
+    with pytest.raises(ValueError):
+        base.verify(2).verify(2)

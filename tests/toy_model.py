@@ -150,6 +150,50 @@ class ToyModel:
         return (h[-1:] @ W["lm_head.weight"].T)[0]
 
 
+    def forward_tokens(self, tokens: List[int], positions: List[int], caches, attend) -> torch.Tensor:
+        """A flattened multi-sequence batch (Attention.forward_batched,
+        model.py:219-247, and forward_all_logits): every layer calls
+        ``attend(cache, q, k, v)`` with K already rotated, which writes K/V
+        and returns the attention output [n, Hq, D]; logits [n, vocab] of
+        every row."""
+        W = self.w
+        ids = torch.tensor(tokens, dtype=torch.long, device=self.device)
+        pos = torch.tensor(positions, dtype=torch.long, device=self.device)
+        n = len(tokens)
+        h = W["embed_tokens.weight"][ids]
+        for li, cache in enumerate(caches):
+            pre = f"layers.{li}."
+            x = self._norm(h, W[pre + "input_layernorm.weight"])
+            q = (x @ W[pre + "self_attn.q_proj.weight"].T).view(n, self.nq, self.hd)
+            k = (x @ W[pre + "self_attn.k_proj.weight"].T).view(n, self.nkv, self.hd)
+            v = (x @ W[pre + "self_attn.v_proj.weight"].T).view(n, self.nkv, self.hd)
+            q, k = self._rope(q, pos), self._rope(k, pos)
+            o = attend(cache, q, k, v).reshape(n, -1)
+            h = h + o @ W[pre + "self_attn.o_proj.weight"].T
+            x = self._norm(h, W[pre + "post_attention_layernorm.weight"])
+            m = F.silu(x @ W[pre + "mlp.gate_proj.weight"].T) * (x @ W[pre + "mlp.up_proj.weight"].T)
+            h = h + m @ W[pre + "mlp.down_proj.weight"].T
+        h = self._norm(h, W["norm.weight"])
+        return h @ W["lm_head.weight"].T
+
+
+def int4_draft_weights(weights: Dict[str, torch.Tensor]) -> Dict[str, torch.Tensor]:
+    """A stand-in for helios' int4 draft view (exec/qassd.py:153-181): every
+    decoder-layer Linear weight rounded to 16 symmetric levels per output
+    row, s = absmax / 7, w = clamp(round(w / s), -8, 7) * s.  helios'
+    quantize_model is weight quantization, outside the attention path; the
+    speculative tests only need a draft that disagrees with the target now
+    and then, since the committed tokens must equal the target's greedy
+    tokens whatever the draft proposes (tests/quant/test_qassd.py:147-193)."""
+    out = {}
+    for name, w in weights.items():
+        if name.startswith("layers.") and w.dim() == 2:
+            s = w.abs().amax(dim=1, keepdim=True).clamp_min(1e-8) / 7.0
+            w = torch.clamp(torch.round(w / s), -8, 7) * s
+        out[name] = w
+    return out
+
+
 def greedy(model: ToyModel, attn: AttentionBackend, prompt: List[int], n_new: int,
            block_table: List[int]) -> List[int]:
     """Engine-style greedy generation: one prefill of the prompt, then one
@@ -174,4 +218,5 @@ def checksums(weights: Dict[str, torch.Tensor]) -> Dict[str, tuple]:
     return {k: (float(v.double().sum()), float((v.double() ** 2).sum())) for k, v in weights.items()}
 
 
-__all__ = ["TOY", "toy_weights", "ToyModel", "AttentionBackend", "greedy", "checksums"]
+__all__ = ["TOY", "toy_weights", "ToyModel", "AttentionBackend", "greedy", "checksums",
+           "int4_draft_weights"]
