@@ -24,9 +24,10 @@ struct PrefillArgs {
   float scale_log2;
 };
 
-// LDS-tiled 32x32 MFMA prefill for fp16 / bf16 pools with head_dim 64 or 128
-// and block_size >= 16; returns false (launching nothing) for other shapes.
-bool launch_prefill_mfma(const PrefillArgs& a, int q_dtype, int kv_dtype, int head_dim,
+// LDS-tiled 32x32 MFMA prefill for fp16 / bf16 queries over pools of the
+// same dtype or int8 pools (fp16 / fp32 scales), head_dim 64 or 128 and
+// block_size >= 16; returns false (launching nothing) for other shapes.
+bool launch_prefill_mfma(const PrefillArgs& a, int q_dtype, int kv_dtype, int scale_dtype, int head_dim,
                          int max_q_len, hipStream_t s);
 
 }  // namespace hpa

@@ -35,6 +35,15 @@
 // conflict-free for 64 banks and for 32.  The global->LDS loads apply the
 // inverse permutation on the global side, so the per-lane LDS destinations
 // stay the hardware's consecutive ones.
+//
+// INT8 pools (QuantizedPagedKVCache) run the same MFMA path on dequantised
+// tiles.  The int8 K/V rows of a step and their per-(token, head) scales are
+// copied into LDS stages by the same direct loads; one step ahead of the
+// compute, each wave dequantises exactly the 16 keys of one tensor it copied
+// (so only its own load count, no barrier, guards the read) into one of two
+// fp16/bf16 tiles laid out and swizzled like the fp16 path's, as
+// (q * s).to(dtype) -- the reference's gather, exec/paged_attn.py:213-235.
+// The step's barrier then publishes that tile and frees the other one.
 #include <type_traits>
 
 #include "hpa_attn_core.h"
@@ -74,6 +83,44 @@ template <> struct M32<BF16> {
   __device__ __forceinline__ static float lo_of(uint32_t w) { return bf16_bits_to_f32(w & 0xffffu); }
   __device__ __forceinline__ static float hi_of(uint32_t w) { return bf16_bits_to_f32(w >> 16); }
 };
+
+// (q * s).to(CT) of the 4 NW int8 values in `in` (little-endian bytes) with
+// one scale (raw ST bits), two values per output word: the reference's
+// dequantisation, exec/paged_attn.py:213-235 (fp32 product, then the
+// compute dtype).  Each value is rounded once, as there.
+template <class CT, class ST, int NW>
+__device__ __forceinline__ void dequant_words(const uint32_t* in, uint32_t sbits, uint32_t* out) {
+#pragma clang fp contract(off)
+  if constexpr (std::is_same<CT, F16>::value && std::is_same<ST, F16>::value) {
+    // [q ^ 0x80, 0x64] is the fp16 value 1152 + q; less 1152 is q exactly,
+    // and the fp16 product with the fp16 scale is q * s rounded once to fp16
+    // (the fp32 product of an 8-bit and an 11-bit significand is exact)
+    const f16x2 off = {(_Float16)-1152.f, (_Float16)-1152.f};
+    const f16x2 sv = __builtin_bit_cast(f16x2, (sbits & 0xffffu) * 0x10001u);
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const uint32_t x = in[w] ^ 0x80808080u;
+      const f16x2 lo = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, x, 0x04010400u)) + off;
+      const f16x2 hi = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, x, 0x04030402u)) + off;
+      out[2 * w] = __builtin_bit_cast(uint32_t, lo * sv);
+      out[2 * w + 1] = __builtin_bit_cast(uint32_t, hi * sv);
+    }
+  } else {
+    // fp32: byte q ^ 0x80 = q + 128 exactly; fma(q + 128, s, -128 s) is
+    // q * s rounded once (-128 s is exact), then rounded to CT
+    const float s = std::is_same<ST, F16>::value ? f16_bits_to_f32(sbits & 0xffffu) : __builtin_bit_cast(float, sbits);
+    const float c = -128.f * s;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const uint32_t x = in[w] ^ 0x80808080u;
+      float f[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) f[k] = __builtin_fmaf((float)((x >> (8 * k)) & 0xffu), s, c);
+      out[2 * w] = M32<CT>::pack(f[0], f[1]);
+      out[2 * w + 1] = M32<CT>::pack(f[2], f[3]);
+    }
+  }
+}
 
 constexpr int kPfWaves = 4;              // waves per workgroup, 32 rows each
 constexpr int kPfRows = 32 * kPfWaves;   // rows per workgroup
@@ -122,21 +169,32 @@ __device__ __forceinline__ float pair_sum(float x) {
   return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
 }
 
-template <class CT, int D>
+template <class CT, class KVT, class ST, int D>
 __global__ __launch_bounds__(64 * kPfWaves, 2) void prefill_mfma_kernel(const PrefillArgs a,
                                                                      const int32_t* __restrict__ tables,
                                                                      int tiles_per_unit) {
   typedef M32<CT> M;
   typedef typename CT::storage q_t;
+  constexpr bool QUANT = std::is_same<KVT, I8>::value;
   constexpr int NCH = D / 8;          // 16-byte chunks per key row
   constexpr int ROWB = D * 2;         // bytes per key row
   constexpr int TILEB = 32 * ROWB;    // one 32-key tile of K or of V
   constexpr int KCH = D / 16;         // QK MFMAs per step
   constexpr int DB = D / 32;          // PV MFMAs per 16-key chunk: O^T block db = dims [32db, 32db + 32)
   constexpr int IPW = NCH / 4;        // global->LDS instructions per wave per step
+  // int8: a wave copies 16 keys x D bytes (R8) plus one scale per lane, and
+  // dequantises them; NS stages run NS - 2 steps ahead of the dequantisation
+  constexpr int R8 = 16 * D;
+  constexpr int IPW8 = R8 / 1024;
+  constexpr int G8 = IPW8 + 1;        // loads per wave per step
+  constexpr int NS = QUANT ? 5 : kPfStages;
+  constexpr int SSZ = QUANT ? (int)sizeof(typename ST::storage) : 4;
   static_assert(D == 64 || D == 128, "head_dim 64 or 128");
   static_assert(kPfStages == 3 || kPfStages == 4, "waits below cover up to two later steps in flight");
-  __shared__ __attribute__((aligned(16))) uint8_t smem[kPfStages][2 * TILEB];
+  // fp pools: NS stages of [K tile | V tile].  int8 pools: two dequantised
+  // [K tile | V tile] buffers, then NS int8 stages of 4 wave regions.
+  constexpr int SMEM = QUANT ? 2 * 2 * TILEB + NS * 4 * R8 : NS * 2 * TILEB;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[SMEM];
 
   // ---- which (unit, row tile) this workgroup runs: longest-first per XCD
   const int units = a.num_seqs * a.num_kv_heads;
@@ -146,7 +204,7 @@ __global__ __launch_bounds__(64 * kPfWaves, 2) void prefill_mfma_kernel(const Pr
     const int xcd = item & 7, m = item >> 3;
     const int nk = ((int)gridDim.x - xcd + 7) >> 3;  // items on this XCD
     if (nk <= kPfLptMax) {
-      int* cost = reinterpret_cast<int*>(&smem[0][0]);
+      int* cost = reinterpret_cast<int*>(&smem[0]);
       for (int j = threadIdx.x; j < nk; j += 64 * kPfWaves) cost[j] = item_cost(a, 8 * j + xcd, units, tiles_per_unit);
       __syncthreads();
       for (int j = threadIdx.x; j < nk; j += 64 * kPfWaves) {
@@ -213,6 +271,8 @@ __global__ __launch_bounds__(64 * kPfWaves, 2) void prefill_mfma_kernel(const Pr
     voff[i] = (uint32_t)((row & 15) * ROWB + (q ^ swz) * 16);
   }
   const char* pool = reinterpret_cast<const char*>(tensor ? a.v : a.k);
+  const char* spool = reinterpret_cast<const char*>(tensor ? a.vs : a.ks);
+  uint32_t sc[NS];  // int8: this lane's key scale, per stage (raw bits)
   const long blk_rows = (long)a.num_kv_heads << a.bs_log2;   // key rows per block
   const long head_rows = (long)kvh << a.bs_log2;
   const int bsm = (1 << a.bs_log2) - 1;
@@ -229,19 +289,72 @@ __global__ __launch_bounds__(64 * kPfWaves, 2) void prefill_mfma_kernel(const Pr
       phys = win.get(lb);
       if ((unsigned)phys >= (unsigned)a.num_blocks) { phys = 0; valid = 0; }
     }
-    const char* base = pool + ((long)phys * blk_rows + head_rows + (key0 & bsm)) * ROWB;
-    // the record count is computed on the VALU (min/max); pinning it to a
-    // scalar keeps the resource uniform, with no per-lane loop around the loads
-    const int nbytes = __builtin_amdgcn_readfirstlane(valid * ROWB);
-    const __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), (short)0, nbytes, 0x00020000);
+    if constexpr (QUANT) {
+      // 16 consecutive int8 rows of one block, copied as they lie: lane l's
+      // 16 bytes of instruction i land at region + 1024 i + 16 l
+      const long row0 = (long)phys * blk_rows + head_rows + (key0 & bsm);
+      const int nbytes = __builtin_amdgcn_readfirstlane(valid * D);
+      const __amdgpu_buffer_rsrc_t rs =
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(pool + row0 * D), (short)0, nbytes, 0x00020000);
+      uint8_t* dst = &smem[2 * 2 * TILEB + stage * 4 * R8 + w * R8];
 #pragma unroll
-    for (int i = 0; i < IPW; ++i) {
-      // a local copy: the host pass of this builtin rejects a captured array
-      // element, which would silently drop the kernel's launch stub
-      const int vo = (int)voff[i];
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rs, (__attribute__((address_space(3))) void*)(&smem[stage][0] + (w * IPW + i) * 64 * 16), 16, vo, 0, 0, 0);
+      for (int i = 0; i < IPW8; ++i)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(dst + i * 1024), 16,
+                                                 i * 1024 + lane * 16, 0, 0, 0);
+      // the scale of the key this lane dequantises (key lane / 4); rows past
+      // the context read as 0
+      const int sbytes = __builtin_amdgcn_readfirstlane(valid * SSZ);
+      const __amdgpu_buffer_rsrc_t srs =
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(spool + row0 * SSZ), (short)0, sbytes, 0x00020000);
+      if constexpr (SSZ == 2)
+        sc[stage] = __builtin_amdgcn_raw_buffer_load_b16(srs, (lane >> 2) * 2, 0, 0);
+      else
+        sc[stage] = __builtin_amdgcn_raw_buffer_load_b32(srs, (lane >> 2) * 4, 0, 0);
+    } else {
+      const char* base = pool + ((long)phys * blk_rows + head_rows + (key0 & bsm)) * ROWB;
+      // the record count is computed on the VALU (min/max); pinning it to a
+      // scalar keeps the resource uniform, with no per-lane loop around the loads
+      const int nbytes = __builtin_amdgcn_readfirstlane(valid * ROWB);
+      const __amdgpu_buffer_rsrc_t rs =
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), (short)0, nbytes, 0x00020000);
+#pragma unroll
+      for (int i = 0; i < IPW; ++i) {
+        // a local copy: the host pass of this builtin rejects a captured array
+        // element, which would silently drop the kernel's launch stub
+        const int vo = (int)voff[i];
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rs, (__attribute__((address_space(3))) void*)(&smem[stage * 2 * TILEB] + (w * IPW + i) * 64 * 16), 16, vo,
+            0, 0, 0);
+      }
+    }
+  };
+
+  // int8: dequantise this wave's 16 keys of step j (stage `stage`) into the
+  // compute tile of step j.  Lane l holds key 16 half + l / 4, dims
+  // [(l % 4) D / 4, +D / 4), written as D / 32 swizzled 16-byte chunks.
+  auto dequant = [&](int j, int stage) {
+    if constexpr (QUANT) {
+      constexpr int BPL = D / 4;   // int8 bytes per lane
+      const uint8_t* src = &smem[2 * 2 * TILEB + stage * 4 * R8 + w * R8 + lane * BPL];
+      uint32_t in[BPL / 4];
+#pragma unroll
+      for (int c = 0; c < BPL / 16; ++c) {
+        const u32x4 x = *reinterpret_cast<const u32x4*>(src + 16 * c);
+        in[4 * c] = x[0];
+        in[4 * c + 1] = x[1];
+        in[4 * c + 2] = x[2];
+        in[4 * c + 3] = x[3];
+      }
+      uint32_t outw[BPL / 2];
+      dequant_words<CT, ST, BPL / 4>(in, sc[stage], outw);
+      const int row = 16 * half + (lane >> 2);
+      const int swz = tensor ? v_swz(NCH, row) : row % NCH;
+      uint8_t* tile = &smem[(j & 1) * 2 * TILEB + tensor * TILEB + row * ROWB];
+      const int jc0 = (lane & 3) * (D / 32);
+#pragma unroll
+      for (int c = 0; c < D / 32; ++c)
+        *reinterpret_cast<u32x4*>(tile + ((jc0 + c) ^ swz) * 16) =
+            (u32x4){outw[4 * c], outw[4 * c + 1], outw[4 * c + 2], outw[4 * c + 3]};
     }
   };
 
@@ -273,15 +386,28 @@ __global__ __launch_bounds__(64 * kPfWaves, 2) void prefill_mfma_kernel(const Pr
   // one step: wait for its copies, barrier, issue the copies kPfStages - 1
   // steps ahead, then compute (STAGE folds to a constant in every unrolled call)
   auto step = [&](int i, const int STAGE) {
-    // this wave's copies for step i have landed once at most the later
-    // steps' groups (IPW loads each) are still in flight
-    const int later = min(nsteps - 1 - i, kPfStages - 2);
-    if (later >= 2) {
-      __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * IPW));  // vmcnt(2 IPW)
-    } else if (later == 1) {
-      __builtin_amdgcn_s_waitcnt(0x0F70 | IPW);        // vmcnt(IPW)
+    if constexpr (QUANT) {
+      // this wave's copies for step i + 1 (dequantised below) have landed
+      // once at most the later steps' groups (G8 loads each) are in flight
+      const int later = min(nsteps - 2 - i, NS - 3);
+      if (later >= 2) {
+        __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * G8));
+      } else if (later == 1) {
+        __builtin_amdgcn_s_waitcnt(0x0F70 | G8);
+      } else {
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+      }
     } else {
-      __builtin_amdgcn_s_waitcnt(0x0F70);              // vmcnt(0)
+      // this wave's copies for step i have landed once at most the later
+      // steps' groups (IPW loads each) are still in flight
+      const int later = min(nsteps - 1 - i, kPfStages - 2);
+      if (later >= 2) {
+        __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * IPW));  // vmcnt(2 IPW)
+      } else if (later == 1) {
+        __builtin_amdgcn_s_waitcnt(0x0F70 | IPW);        // vmcnt(IPW)
+      } else {
+        __builtin_amdgcn_s_waitcnt(0x0F70);              // vmcnt(0)
+      }
     }
     // After the barrier every wave's copies for step i are in LDS (each
     // waited for its own above) and every wave has consumed its reads of
@@ -292,10 +418,15 @@ __global__ __launch_bounds__(64 * kPfWaves, 2) void prefill_mfma_kernel(const Pr
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_barrier();
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    if (i + kPfStages - 1 < nsteps) issue_loads(i + kPfStages - 1, (STAGE + kPfStages - 1) % kPfStages);
+    // int8: the barrier also published the tile of step i (dequantised in
+    // step i - 1) and retired every read of the tile step i + 1 reuses
+    if (i + NS - 1 < nsteps) issue_loads(i + NS - 1, (STAGE + NS - 1) % NS);
+    if constexpr (QUANT) {
+      if (i + 1 < nsteps) dequant(i + 1, (STAGE + 1) % NS);
+    }
     const int k0 = 32 * i;
     if (k0 >= wave_maxlim) return;
-    const uint8_t* st_base = &smem[STAGE][0];
+    const uint8_t* st_base = QUANT ? &smem[(i & 1) * 2 * TILEB] : &smem[STAGE * 2 * TILEB];
 
     // ---- S^T = K . Q^T
     f32x16 st = (f32x16){};
@@ -374,11 +505,28 @@ __global__ __launch_bounds__(64 * kPfWaves, 2) void prefill_mfma_kernel(const Pr
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 #pragma unroll
-  for (int u = 0; u < kPfStages - 1; ++u)
+  for (int u = 0; u < NS - 1; ++u)
     if (u < nsteps) issue_loads(u, u);
-  for (int i0 = 0; i0 < nsteps; i0 += kPfStages) {
+  if constexpr (QUANT) {
+    // step 0's tile: this wave's copies for step 0 landed once at most the
+    // later groups are in flight
+    if (nsteps > 0) {
+      const int later = min(nsteps - 1, NS - 2);
+      if (later >= 3) {
+        __builtin_amdgcn_s_waitcnt(0x0F70 | (3 * G8));
+      } else if (later == 2) {
+        __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * G8));
+      } else if (later == 1) {
+        __builtin_amdgcn_s_waitcnt(0x0F70 | G8);
+      } else {
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+      }
+      dequant(0, 0);
+    }
+  }
+  for (int i0 = 0; i0 < nsteps; i0 += NS) {
 #pragma unroll
-    for (int u = 0; u < kPfStages; ++u)
+    for (int u = 0; u < NS; ++u)
       if (i0 + u < nsteps) step(i0 + u, u);
   }
 
@@ -402,30 +550,39 @@ __global__ __launch_bounds__(64 * kPfWaves, 2) void prefill_mfma_kernel(const Pr
 }
 
 
-template <class CT, int D>
+template <class CT, class KVT, class ST, int D>
 static void launch_one(const PrefillArgs& a, int max_q_len, hipStream_t s) {
   const int units = a.num_seqs * a.num_kv_heads;
   const int tiles = (max_q_len * a.group + kPfRows - 1) / kPfRows;
-  hipLaunchKernelGGL((prefill_mfma_kernel<CT, D>), dim3((unsigned)(units * tiles)), dim3(64 * kPfWaves),
+  hipLaunchKernelGGL((prefill_mfma_kernel<CT, KVT, ST, D>), dim3((unsigned)(units * tiles)), dim3(64 * kPfWaves),
                      0, s, a, a.tables, tiles);
 }
 
-bool launch_prefill_mfma(const PrefillArgs& a, int q_dtype, int kv_dtype, int head_dim, int max_q_len,
-                         hipStream_t s) {
-  if (a.bs_log2 < 4 || kv_dtype != q_dtype || (head_dim != 64 && head_dim != 128)) return false;
+template <class CT, class KVT, class ST>
+static bool launch_d(const PrefillArgs& a, int head_dim, int max_q_len, hipStream_t s) {
+  if (head_dim == 128) launch_one<CT, KVT, ST, 128>(a, max_q_len, s);
+  else launch_one<CT, KVT, ST, 64>(a, max_q_len, s);
+  return true;
+}
+
+template <class CT>
+static bool launch_ct(const PrefillArgs& a, int kv_dtype, int scale_dtype, int head_dim, int max_q_len,
+                      hipStream_t s) {
+  if (kv_dtype == CT::code) return launch_d<CT, CT, F32>(a, head_dim, max_q_len, s);
+  if (kv_dtype != HPA_I8 || !a.ks || !a.vs) return false;
+  if (scale_dtype == HPA_F16) return launch_d<CT, I8, F16>(a, head_dim, max_q_len, s);
+  if (scale_dtype == HPA_F32) return launch_d<CT, I8, F32>(a, head_dim, max_q_len, s);
+  return false;
+}
+
+bool launch_prefill_mfma(const PrefillArgs& a, int q_dtype, int kv_dtype, int scale_dtype, int head_dim,
+                         int max_q_len, hipStream_t s) {
+  if (a.bs_log2 < 4 || (head_dim != 64 && head_dim != 128)) return false;
   if ((long)max_q_len * a.group > (1L << 30)) return false;
   if ((long)a.num_seqs * a.num_kv_heads * ((max_q_len * (long)a.group + kPfRows - 1) / kPfRows) > 0x7fffffffL)
     return false;
-  if (q_dtype == HPA_F16) {
-    if (head_dim == 128) launch_one<F16, 128>(a, max_q_len, s);
-    else launch_one<F16, 64>(a, max_q_len, s);
-    return true;
-  }
-  if (q_dtype == HPA_BF16) {
-    if (head_dim == 128) launch_one<BF16, 128>(a, max_q_len, s);
-    else launch_one<BF16, 64>(a, max_q_len, s);
-    return true;
-  }
+  if (q_dtype == HPA_F16) return launch_ct<F16>(a, kv_dtype, scale_dtype, head_dim, max_q_len, s);
+  if (q_dtype == HPA_BF16) return launch_ct<BF16>(a, kv_dtype, scale_dtype, head_dim, max_q_len, s);
   return false;
 }
 

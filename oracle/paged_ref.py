@@ -8,6 +8,8 @@ Every function follows the reference file:line it cites (reference =
 anish41338/helios, python/helios/exec/paged_attn.py unless stated).  How
 each one is pinned (tests/test_oracle.py):
 
+  round_bf16               torch's own float32 -> bfloat16 conversion on
+                           random values, ties and carries into the exponent
   quantize / store_scale   closed form + hand-built round-half-even ties,
                            clamp and zero-row cases, an independent float64
                            division, and the round-trip bound of the
@@ -69,9 +71,20 @@ def store_scale(scale: np.ndarray, scale_dtype=np.float16) -> np.ndarray:
 
 def dequantize(q: np.ndarray, s_stored: np.ndarray, out_dtype=np.float32) -> np.ndarray:
     """QuantizedPagedKVCache.gather's deq (paged_attn.py:228-233):
-    (q.float() * s.float()).to(dtype)."""
+    (q.float() * s.float()).to(dtype).  out_dtype "bfloat16" rounds to
+    bfloat16 (returned as the float32 values it represents)."""
     prod = q.astype(F32) * np.asarray(s_stored).astype(F32)[..., None]
+    if isinstance(out_dtype, str) and out_dtype == "bfloat16":
+        return round_bf16(prod)
     return prod.astype(out_dtype)
+
+
+def round_bf16(x: np.ndarray) -> np.ndarray:
+    """float32 -> bfloat16, round to nearest even (torch's .to(torch.bfloat16)),
+    as float32.  Finite inputs only."""
+    u = np.asarray(x, dtype=F32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return u.astype(np.uint32).view(F32)
 
 
 # ------------------------------------------------------------------ KV pool

@@ -54,6 +54,18 @@ def pool_of(cache) -> R.PagedPool:
     return p
 
 
+def pool_dequantized(cache) -> R.PagedPool:
+    """numpy mirror of an int8 cache as helios' gather hands it to attention:
+    (q.float() * s.float()).to(compute dtype) (paged_attn.py:213-235), held
+    as the float32 values those fp16 / bf16 numbers represent.  The MFMA
+    prefill kernel attends over exactly these values."""
+    out = {torch.float16: np.float16, torch.bfloat16: "bfloat16"}[cache.dtype]
+    p = R.PagedPool(cache.num_blocks, cache.block_size, cache.n_kv_heads, cache.head_dim, np.float32)
+    p.k = R.dequantize(to_np(cache.k_cache), to_np(cache.k_scale), out).astype(np.float32)
+    p.v = R.dequantize(to_np(cache.v_cache), to_np(cache.v_scale), out).astype(np.float32)
+    return p
+
+
 def ragged_tables(gen: np.random.Generator, lens, block_size, num_blocks, shuffle=True):
     """Non-contiguous block tables from a (shuffled) pool."""
     need = [(c + block_size - 1) // block_size for c in lens]

@@ -15,7 +15,7 @@ from helios_amd import (
     paged_attention_verify_batched,
 )
 from oracle import paged_ref as R
-from tests.gpu_util import dev, fill_cache, pool_of, ragged_tables, to_np
+from tests.gpu_util import dev, fill_cache, pool_dequantized, pool_of, ragged_tables, to_np
 from tests.test_gpu_decode import _check
 
 pytestmark = pytest.mark.gpu
@@ -70,8 +70,50 @@ def test_varlen_int8(scale_dtype):
                                 scale_dtype=scale_dtype)
     q = torch.randn(sum(qlens), 32, 128, generator=gen).half().to(dev())
     got = paged_attention_varlen(q, cache, tables, qlens, starts, ctxs)
-    want = R.paged_varlen(to_np(q).astype(np.float32), pool_of(cache), tables, qlens, starts, ctxs)
+    # the MFMA kernel attends over helios' fp16 gather of the int8 pool
+    want = R.paged_varlen(to_np(q).astype(np.float32), pool_dequantized(cache), tables, qlens, starts, ctxs)
     _check(got, want, torch.float16)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("scale_dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("D,bs", [(128, 16), (64, 32)])
+def test_mfma_prefill_int8(dtype, scale_dtype, D, bs):
+    """INT8 pools on the MFMA kernel: ragged chunks, partial last blocks,
+    contexts shorter than a step, several steps per row tile."""
+    qlens = [1, 37, 130, 9, 64]
+    starts = [3, 0, 250, 64, 700]
+    ctxs = [s + n for s, n in zip(starts, qlens)]
+    cache, tables, gen = _setup(D + bs, ctxs, 16, 4, D, bs, dtype, quant=True, scale_dtype=scale_dtype)
+    q = torch.randn(sum(qlens), 16, D, generator=gen).to(dtype).to(dev())
+    got = paged_attention_varlen(q, cache, tables, qlens, starts, ctxs)
+    want = R.paged_varlen(to_np(q).astype(np.float32), pool_dequantized(cache), tables, qlens, starts, ctxs)
+    _check(got, want, dtype, f"int8 {dtype} scales {scale_dtype} D={D} bs={bs}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("scale_dtype", [torch.float16, torch.float32])
+def test_mfma_int8_dequantisation_is_helios_gather(dtype, scale_dtype):
+    """With one key in context every query row's output is that key's V row
+    (p = 1), so the kernel's dequantisation shows bit for bit: it must equal
+    (q.float() * s.float()).to(dtype), helios' gather (paged_attn.py:228-233),
+    for every int8 value and scales across the fp16 range."""
+    H, D, bs = 2, 128, 16
+    cache = QuantizedPagedKVCache(4, bs, H, D, dtype=dtype, device="cuda", scale_dtype=scale_dtype)
+    gen = torch.Generator().manual_seed(1)
+    cache.k_cache.copy_(torch.randint(-127, 128, cache.k_cache.shape, generator=gen, dtype=torch.int8))
+    v = torch.randint(-127, 128, cache.v_cache.shape, generator=gen, dtype=torch.int8)
+    v[2, 0, 0, :] = torch.arange(-127, 1, dtype=torch.int8)[:D]      # every value appears
+    v[2, 1, 0, :] = torch.arange(0, 128, dtype=torch.int8)[:D]
+    cache.v_cache.copy_(v)
+    # 2^-22 .. 2^8: products from fp16 subnormals up to 127 * 256, all finite
+    scales = torch.exp2(torch.rand(cache.v_scale.shape, generator=gen) * 30 - 22)
+    cache.k_scale.copy_(scales.to(scale_dtype))
+    cache.v_scale.copy_(scales.flip(-1).to(scale_dtype))
+    q = torch.randn(1, 8, D, generator=gen).to(dtype).to(dev())
+    got = paged_attention_varlen(q, cache, [[2]], [1], [0], [1])
+    want = (cache.v_cache[2, :, 0, :].float() * cache.v_scale[2, :, 0, None].float()).to(dtype)
+    assert torch.equal(got[0].view(H, 4, D), want[:, None, :].expand(H, 4, D))
 
 
 def test_chunked_prefill_equals_single_shot():
@@ -126,9 +168,12 @@ def test_verify_kernels_agree():
     a = paged_attention_verify_batched(q, cache, tables, lens, 3)
     b = paged_attention_varlen(q, cache, tables, [3] * 3, [c - 3 for c in lens], lens)
     assert (a.float() - b.float()).abs().max().item() <= 2e-3
+    # the decode kernel dequantises exactly in fp32; the MFMA prefill attends
+    # over helios' fp16 gather of the same int8 pool
     want = R.paged_verify_batched(to_np(q).astype(np.float32), pool_of(cache), tables, lens, 3)
     _check(a, want, torch.float16)
-    _check(b, want, torch.float16)
+    want_b = R.paged_verify_batched(to_np(q).astype(np.float32), pool_dequantized(cache), tables, lens, 3)
+    _check(b, want_b, torch.float16)
 
 
 def test_rows_without_keys_are_zero():

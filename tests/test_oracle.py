@@ -14,6 +14,7 @@ import math
 
 import numpy as np
 import pytest
+import torch
 
 from oracle import paged_ref as R
 
@@ -360,3 +361,14 @@ def test_rope_table_restatement_close_to_helios():
     cos, sin = _helios_rope_tables(256, 64)
     c2, s2 = R.build_rope_cache(256, 64)
     assert np.abs(cos - c2).max() < 1e-4 and np.abs(sin - s2).max() < 1e-4
+
+
+def test_round_bf16_matches_torch():
+    rng = np.random.default_rng(0)
+    x = np.concatenate([rng.standard_normal(10000).astype(np.float32) * 10.0 ** rng.integers(-8, 8, 10000),
+                        # exact ties (low half 0x8000) with even and odd kept bits, and a carry
+                        np.array([0x3F808000, 0x3F818000, 0x3F7FFFFF, 0x7F7F8000 - 0x10000], np.uint32).view(np.float32)])
+    want = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    np.testing.assert_array_equal(R.round_bf16(x), want)
+    # hand example: 1 + 2^-8 is a tie between 1 and 1 + 2^-7, even (1) wins
+    assert R.round_bf16(np.float32(1 + 2 ** -8)) == 1.0
