@@ -223,13 +223,15 @@ class PrefillWorkload(Workload):
 
     bound = "mfma"
 
-    def __init__(self, device, seed):
+    def __init__(self, device, seed, kv_int8=False):
         import numpy as np
         import torch
 
         import helios_amd as H
 
-        self.name = "llama3-8b-fp16-chunked-prefill (config 4)"
+        self.kv_int8 = kv_int8
+        self.name = ("llama3-8b-int8-kv-chunked-prefill (config 4 shape, int8 pool)" if kv_int8
+                     else "llama3-8b-fp16-chunked-prefill (config 4)")
         rng = np.random.default_rng(seed)
         gen = torch.Generator(device=device).manual_seed(seed)
         B, Hq, Hkv, D, T = 8, 32, 8, 128, 512
@@ -256,6 +258,16 @@ class PrefillWorkload(Workload):
         self.cache = H.PagedKVCache(nb, BLOCK, Hkv, D, dtype=torch.float16, device=device)
         for t in (self.cache.k_cache, self.cache.v_cache):
             t.normal_(generator=gen)
+        if kv_int8:
+            # the same values quantized by the library's write kernel, every
+            # block written as one run of nb x 16 tokens
+            fp = self.cache
+            self.cache = H.QuantizedPagedKVCache(nb, BLOCK, Hkv, D, dtype=torch.float16, device=device,
+                                                 scale_dtype=torch.float16)
+            flat = [t.permute(0, 2, 1, 3).reshape(nb * BLOCK, Hkv, D) for t in (fp.k_cache, fp.v_cache)]
+            H.write_kv(self.cache, [list(range(nb))], [0], flat[0], flat[1])
+            del fp, flat
+            torch.cuda.synchronize()
         self.q = torch.randn(B * T, Hq, D, generator=gen, device=device, dtype=torch.float16)
         self.qlens = torch.full((B,), T, dtype=torch.int32, device=device)
         self.cu = torch.arange(0, (B + 1) * T, T, dtype=torch.int32, device=device)
@@ -264,7 +276,8 @@ class PrefillWorkload(Workload):
         self.scale = 1.0 / math.sqrt(D)
         self.flops = 4 * D * Hq * sum(sum(p + i + 1 for i in range(T)) for p in priors)
         n_tab = sum(need)
-        self.alg_bytes = sum(ctxs) * 2 * Hkv * D * 2 + 2 * B * T * Hq * D * 2 + 4 * n_tab
+        kvb = D + 2 if kv_int8 else 2 * D
+        self.alg_bytes = sum(ctxs) * 2 * Hkv * kvb + 2 * B * T * Hq * D * 2 + 4 * n_tab
         self.tokens = B * T
 
     def step(self):
@@ -277,7 +290,8 @@ class PrefillWorkload(Workload):
     def config(self):
         return {"workload": self.name, "sequences": self.B, "chunk": self.T,
                 "n_q_heads": self.Hq, "n_kv_heads": self.Hkv, "head_dim": self.D,
-                "block_size": BLOCK, "kv_dtype": "fp16", "prior_context": self.priors,
+                "block_size": BLOCK, "kv_dtype": "int8" if self.kv_int8 else "fp16",
+                "prior_context": self.priors,
                 "shared_prefix_blocks": 64}
 
     def cpu_baseline(self, budget_s):
@@ -285,9 +299,15 @@ class PrefillWorkload(Workload):
 
         from oracle import paged_ref as R
 
-        pool = R.PagedPool(self.cache.num_blocks, BLOCK, self.Hkv, self.D, np.float32)
-        pool.k = self.cache.k_cache.float().cpu().numpy()
-        pool.v = self.cache.v_cache.float().cpu().numpy()
+        if self.kv_int8:
+            pool = R.PagedPool(self.cache.num_blocks, BLOCK, self.Hkv, self.D, np.float32, quantized=True,
+                               scale_dtype=np.float16)
+            pool.k, pool.v = self.cache.k_cache.cpu().numpy(), self.cache.v_cache.cpu().numpy()
+            pool.k_scale, pool.v_scale = self.cache.k_scale.cpu().numpy(), self.cache.v_scale.cpu().numpy()
+        else:
+            pool = R.PagedPool(self.cache.num_blocks, BLOCK, self.Hkv, self.D, np.float32)
+            pool.k = self.cache.k_cache.float().cpu().numpy()
+            pool.v = self.cache.v_cache.float().cpu().numpy()
         q = self.q.float().cpu().numpy()
         done, t0 = 0, time.perf_counter()
         while done < self.B and time.perf_counter() - t0 < budget_s:
@@ -507,6 +527,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=500)
     ap.add_argument("--config", type=int, default=5, choices=[1, 2, 3, 4, 5])
     ap.add_argument("--seed", type=int, default=None)
+    ap.add_argument("--kv-int8", action="store_true",
+                    help="config 4 on an int8 pool (the same values quantized by the write kernel)")
     ap.add_argument("--part-tokens", type=int, default=0,
                     help="split-K partition size for decode (0 = library default)")
     ap.add_argument("--copies", type=int, default=None,
@@ -559,7 +581,7 @@ def main():
     seed = args.config - 1 if args.seed is None else args.seed
 
     if args.config == 4:
-        wl = PrefillWorkload(device, seed)
+        wl = PrefillWorkload(device, seed, kv_int8=args.kv_int8)
     else:
         copies = args.copies
         if copies is None:
@@ -586,13 +608,13 @@ def main():
         achieved = wl.alg_bytes / (ms * 1e-3) / 1e9
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                "traffic": _traffic(f"config{args.config}"),
+                "traffic": _traffic(f"config{args.config}" + ("_int8" if args.kv_int8 else "")),
                 "algorithmic_bytes": int(wl.alg_bytes)}
     else:
         achieved = wl.flops / (ms * 1e-3) / 1e12
         roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_F16_PEAK_TFS,
                 "unit": "TFLOP/s", "frac": round(achieved / MFMA_F16_PEAK_TFS, 4),
-                "traffic": _traffic(f"config{args.config}"),
+                "traffic": _traffic(f"config{args.config}" + ("_int8" if args.kv_int8 else "")),
                 "algorithmic_flops": int(wl.flops)}
     roof["kernel"] = "decode_kernel" if wl.bound == "hbm" else "prefill_mfma_kernel"
 
@@ -615,7 +637,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8-kv/fp16" if getattr(wl, "quant", False) else
+        "dtype": "int8-kv/fp16" if (getattr(wl, "quant", False) or getattr(wl, "kv_int8", False)) else
         ("f32" if args.config == 1 else "f16"),
         "data": "synthetic (seeded N(0,1); int8 KV quantized on the GPU by the library's write kernel)",
         "config": wl.config(),
