@@ -433,6 +433,60 @@ def meta_bench(device, layers, steps, warmup, seed=4):
     }))
 
 
+def graph_bench(device, cfg, layers, steps, warmup):
+    """One decode step of config `cfg`'s batch through `layers` layers (each
+    with its own pool copy, metadata on the device): launched eagerly, layer
+    by layer, and replayed as one captured HIP graph.  Small batches are
+    where the per-launch cost shows."""
+    import torch
+
+    import helios_amd as H
+
+    wl = DecodeWorkload(cfg, device, cfg - 1, 0, layers)
+    tabs = H.DeviceBlockTables.for_cache(wl.caches[0], wl.B, wl.tables_np.shape[1])
+    tables = [[int(x) for x in row[: (c + BLOCK - 1) // BLOCK]] for row, c in zip(wl.tables_np, wl.lens)]
+    meta = tabs.prepare(range(wl.B), tables, wl.lens, [c - wl.Tq for c in wl.lens], [wl.Tq] * wl.B, True)
+    outs = [torch.empty_like(wl.q) for _ in range(layers)]
+    ks = [c._scales() for c in wl.caches]
+
+    def step():
+        for li, c in enumerate(wl.caches):
+            H.paged_attention_decode_hip(wl.q, c.k_cache, c.v_cache, meta.block_tables, meta.context_lens,
+                                         wl.scale, ks[li][0], ks[li][1], q_per_seq=wl.Tq,
+                                         max_context_len=meta.max_context_len, out=outs[li])
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    torch.cuda.synchronize()
+    res = {}
+    for name, fn in (("eager", step), ("graph", g.replay)):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        res[name] = e0.elapsed_time(e1) / steps
+        print(f"{name}: {res[name] * 1e3 / layers:.2f} us per layer", file=sys.stderr, flush=True)
+    print(json.dumps({
+        "metric": f"decode step over {layers} layers ({wl.name}): eager launches vs one captured HIP graph",
+        "value": round(res["graph"], 4), "unit": "ms/step", "higher_is_better": False,
+        "eager_ms_per_step": round(res["eager"], 4),
+        "graph_us_per_layer": round(res["graph"] * 1e3 / layers, 2),
+        "eager_us_per_layer": round(res["eager"] * 1e3 / layers, 2),
+        "hbm_gbs_graph": round(wl.alg_bytes * layers / (res["graph"] * 1e-3) / 1e9, 1),
+        "steps": steps, "warmup": warmup, "layers": layers,
+        "config": {"workload": wl.name, "batch": wl.B, "q_per_seq": wl.Tq},
+    }))
+
+
 def spec_bench(device, gamma, steps, warmup, seed=4):
     """Attention work of one speculative step for config 5's batch, one
     layer: gamma draft decodes over an int8 KV shadow (each writing its
@@ -538,6 +592,9 @@ def main():
     ap.add_argument("--meta-layers", type=int, default=0, metavar="L",
                     help="only time a decode-verify step over L layers with device-resident "
                          "vs per-layer list metadata, print its own JSON line, and exit")
+    ap.add_argument("--graph-layers", type=int, default=0, metavar="L",
+                    help="only time --config's decode step over L layers, eager vs one captured "
+                         "HIP graph, print its own JSON line, and exit")
     ap.add_argument("--spec-gamma", type=int, default=0, metavar="G",
                     help="only time one speculative step's attention (gamma G, config 5 batch) "
                          "batched vs per sequence, print its own JSON line, and exit")
@@ -572,6 +629,9 @@ def main():
     if not torch.cuda.is_available():
         raise SystemExit("bench.py needs a GPU")
     device = torch.device("cuda:0")
+    if args.graph_layers:
+        graph_bench(device, args.config, args.graph_layers, min(args.steps, 100), min(args.warmup, 20))
+        return
     if args.spec_gamma:
         spec_bench(device, args.spec_gamma, min(args.steps, 50), min(args.warmup, 20))
         return
