@@ -130,17 +130,20 @@ def test_chunked_prefill_equals_single_shot():
     _check(single, want, torch.float16)
 
 
-def test_prefix_shared_blocks_config4_shape():
+@pytest.mark.parametrize("quant", [False, True])
+def test_prefix_shared_blocks_config4_shape(quant):
     """Config 4 in miniature: Llama-8B heads (32/8, D 128), 4 sequences each
     appending a 128-token chunk onto prior context; the first 16 blocks of
-    every table are the same physical blocks (prefix-cache aliasing)."""
+    every table are the same physical blocks (prefix-cache aliasing).  Also
+    on an int8 pool (the MFMA kernel's fused dequantisation)."""
     rng = np.random.default_rng(4)
     gen = torch.Generator().manual_seed(4)
     bs, shared = 16, 16
     priors = [300, 0, 1024, 57]
     chunk = 128
     nb = 400
-    cache = PagedKVCache(nb, bs, 8, 128, dtype=torch.float16, device="cuda")
+    cache = (QuantizedPagedKVCache(nb, bs, 8, 128, dtype=torch.float16, device="cuda") if quant
+             else PagedKVCache(nb, bs, 8, 128, dtype=torch.float16, device="cuda"))
     fill_cache(cache, gen)
     ids = list(rng.permutation(nb))
     prefix = [int(x) for x in ids[:shared]]
@@ -154,8 +157,8 @@ def test_prefix_shared_blocks_config4_shape():
     ctxs = [p + chunk for p in priors]
     q = torch.randn(chunk * len(priors), 32, 128, generator=gen).half().to(dev())
     got = paged_attention_varlen(q, cache, tables, [chunk] * 4, priors, ctxs)
-    want = R.paged_varlen(to_np(q).astype(np.float32), pool_of(cache), tables, [chunk] * 4,
-                          priors, ctxs)
+    want = R.paged_varlen(to_np(q).astype(np.float32), pool_dequantized(cache) if quant else pool_of(cache),
+                          tables, [chunk] * 4, priors, ctxs)
     _check(got, want, torch.float16)
 
 
