@@ -10,7 +10,7 @@
 // of one (sequence, KV head); each wave owns 32 of them, one 32x32 MFMA tile.
 // The workgroup walks the keys in steps of 32.  Every step's K and V tiles
 // (32 keys x head_dim each) are copied once from the paged pool into LDS by
-// direct global->LDS buffer loads issued by all four waves, two steps ahead
+// direct global->LDS buffer loads issued by all four waves, four steps ahead
 // of the compute, and then read by every wave, so each K/V byte leaves L2 once
 // per 128 query rows instead of once per wave.
 //
@@ -124,7 +124,7 @@ __device__ __forceinline__ void dequant_words(const uint32_t* in, uint32_t sbits
 
 constexpr int kPfWaves = 4;              // waves per workgroup, 32 rows each
 constexpr int kPfRows = 32 * kPfWaves;   // rows per workgroup
-constexpr int kPfStages = 4;             // LDS tiles: copies run kPfStages - 1 steps ahead
+constexpr int kPfStages = 5;             // LDS tiles: copies run kPfStages - 1 steps ahead
 constexpr int kPfLazy = 8;               // rescale only when a row max grows by > 2^8
 
 // V-tile chunk swizzle by key row % 4 (chunks_per_row 16 and 8)
@@ -190,7 +190,7 @@ __global__ __launch_bounds__(64 * kPfWaves, 2) void prefill_mfma_kernel(const Pr
   constexpr int NS = QUANT ? 5 : kPfStages;
   constexpr int SSZ = QUANT ? (int)sizeof(typename ST::storage) : 4;
   static_assert(D == 64 || D == 128, "head_dim 64 or 128");
-  static_assert(kPfStages == 3 || kPfStages == 4, "waits below cover up to two later steps in flight");
+  static_assert(kPfStages >= 3 && kPfStages <= 5, "waits below cover up to three later steps in flight");
   // fp pools: NS stages of [K tile | V tile].  int8 pools: two dequantised
   // [K tile | V tile] buffers, then NS int8 stages of 4 wave regions.
   constexpr int SMEM = QUANT ? 2 * 2 * TILEB + NS * 4 * R8 : NS * 2 * TILEB;
@@ -200,7 +200,9 @@ __global__ __launch_bounds__(64 * kPfWaves, 2) void prefill_mfma_kernel(const Pr
   const int units = a.num_seqs * a.num_kv_heads;
   int item = (int)blockIdx.x;
   {
-    __shared__ int s_pick;
+    // the pick lives in the last stage, which is first written after the
+    // first step's barrier (every wave has read the pick by then)
+    int& s_pick = *reinterpret_cast<int*>(&smem[SMEM - 4]);
     const int xcd = item & 7, m = item >> 3;
     const int nk = ((int)gridDim.x - xcd + 7) >> 3;  // items on this XCD
     if (nk <= kPfLptMax) {
@@ -401,7 +403,9 @@ __global__ __launch_bounds__(64 * kPfWaves, 2) void prefill_mfma_kernel(const Pr
       // this wave's copies for step i have landed once at most the later
       // steps' groups (IPW loads each) are still in flight
       const int later = min(nsteps - 1 - i, kPfStages - 2);
-      if (later >= 2) {
+      if (later >= 3) {
+        __builtin_amdgcn_s_waitcnt(0x0F70 | (3 * IPW));  // vmcnt(3 IPW)
+      } else if (later == 2) {
         __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * IPW));  // vmcnt(2 IPW)
       } else if (later == 1) {
         __builtin_amdgcn_s_waitcnt(0x0F70 | IPW);        // vmcnt(IPW)
