@@ -171,3 +171,29 @@ def test_a_step_on_device_metadata_does_not_synchronise():
     finally:
         torch.cuda.set_sync_debug_mode(prev)
     torch.cuda.synchronize()
+
+
+def test_step_tables_c_abi_contract():
+    """hpa_step_tables called directly: a replaced suffix lands in the
+    resident row and the step row, entries past n_blocks read 0, and a row
+    outside the resident array gives an all-zero step row (and writes
+    nothing)."""
+    from helios_amd import _lib
+
+    L = _lib.load_library()
+    resident = torch.arange(4 * 6, dtype=torch.int32, device="cuda").view(4, 6).contiguous()
+    before = resident.clone()
+    # (row, n_blocks, upd_first, upd_count, upd_offset)
+    entries = torch.tensor([[2, 5, 3, 2, 0], [7, 4, 0, 1, 2], [0, 2, 0, 0, 3]], dtype=torch.int32, device="cuda")
+    new_ids = torch.tensor([100, 101, 555], dtype=torch.int32, device="cuda")
+    step = torch.full((3, 6), -1, dtype=torch.int32, device="cuda")
+    st = L.hpa_step_tables(entries.data_ptr(), 3, new_ids.data_ptr(), 3, resident.data_ptr(), 4, 6,
+                           step.data_ptr(), 6, torch.cuda.current_stream().cuda_stream)
+    assert st == 0
+    torch.cuda.synchronize()
+    want_res = before.clone()
+    want_res[2, 3:5] = torch.tensor([100, 101], dtype=torch.int32)
+    assert torch.equal(resident, want_res)
+    assert step[0].tolist() == [12, 13, 14, 100, 101, 0]
+    assert step[1].tolist() == [0] * 6   # row 7 is outside the 4 resident rows
+    assert step[2].tolist() == [0, 1, 0, 0, 0, 0]
