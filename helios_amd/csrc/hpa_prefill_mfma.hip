@@ -187,7 +187,7 @@ __global__ __launch_bounds__(64 * kPfWaves, 2) void prefill_mfma_kernel(const Pr
   constexpr int R8 = 16 * D;
   constexpr int IPW8 = R8 / 1024;
   constexpr int G8 = IPW8 + 1;        // loads per wave per step
-  constexpr int NS = QUANT ? 5 : kPfStages;
+  constexpr int NS = QUANT ? 6 : kPfStages;
   constexpr int SSZ = QUANT ? (int)sizeof(typename ST::storage) : 4;
   static_assert(D == 64 || D == 128, "head_dim 64 or 128");
   static_assert(kPfStages >= 3 && kPfStages <= 5, "waits below cover up to three later steps in flight");
@@ -392,7 +392,9 @@ __global__ __launch_bounds__(64 * kPfWaves, 2) void prefill_mfma_kernel(const Pr
       // this wave's copies for step i + 1 (dequantised below) have landed
       // once at most the later steps' groups (G8 loads each) are in flight
       const int later = min(nsteps - 2 - i, NS - 3);
-      if (later >= 2) {
+      if (later >= 3) {
+        __builtin_amdgcn_s_waitcnt(0x0F70 | (3 * G8));
+      } else if (later == 2) {
         __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * G8));
       } else if (later == 1) {
         __builtin_amdgcn_s_waitcnt(0x0F70 | G8);
@@ -516,7 +518,9 @@ __global__ __launch_bounds__(64 * kPfWaves, 2) void prefill_mfma_kernel(const Pr
     // later groups are in flight
     if (nsteps > 0) {
       const int later = min(nsteps - 1, NS - 2);
-      if (later >= 3) {
+      if (later >= 4) {
+        __builtin_amdgcn_s_waitcnt(0x0F70 | (4 * G8));
+      } else if (later == 3) {
         __builtin_amdgcn_s_waitcnt(0x0F70 | (3 * G8));
       } else if (later == 2) {
         __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * G8));
