@@ -160,6 +160,15 @@ class TableResidency:
             self.mirror[row] = []
             self.free.append(row)
 
+    def invalidate(self, plan: "StepPlan") -> None:
+        """Forget what the rows of a planned step hold (their upload did not
+        happen): their next plan uploads whole tables."""
+        for _, _, _, g in plan.groups:
+            for sid in g.seq_ids:
+                row = self.row.get(sid)
+                if row is not None:
+                    self.mirror[row] = []
+
     def check(self, groups: List[_Group]) -> None:
         ids = [sid for g in groups for sid in g.seq_ids]
         if len(ids) > self.max_seqs:
@@ -366,6 +375,13 @@ class DeviceBlockTables:
 
     def _prepare(self, groups: List[_Group]) -> List[DeviceAttnMeta]:
         plan = self.host.plan(groups)
+        try:
+            return self._upload(plan)
+        except BaseException:
+            self.host.invalidate(plan)
+            raise
+
+    def _upload(self, plan: StepPlan) -> List[DeviceAttnMeta]:
         slot = self._slot
         self._slot ^= 1
         if self._copied[slot] is not None:

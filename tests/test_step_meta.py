@@ -287,3 +287,15 @@ def test_speculative_metadata_derivations_match_the_runner():
         base.verify(17)
     with pytest.raises(ValueError):
         base.verify(2).verify(2)
+
+
+def test_invalidate_forces_whole_tables_next_time():
+    """A step whose upload failed leaves its rows unknown: the next plan
+    re-sends those tables whole, and other rows keep their deltas."""
+    res = TableResidency(4, 8, block_size=16, num_blocks=100)
+    res.plan([make_group([1, 2], [[1, 2, 3], [4, 5]], [40, 20], [39, 19], [1, 1], True)])
+    plan = res.plan([make_group([1], [[1, 2, 3, 6]], [49], [48], [1], True)])
+    assert plan.n_new_ids == 1
+    res.invalidate(plan)
+    again = res.plan([make_group([1, 2], [[1, 2, 3, 6], [4, 5]], [49, 20], [48, 19], [1, 1], True)])
+    assert again.n_new_ids == 4  # sequence 1 whole, sequence 2 unchanged
