@@ -446,12 +446,14 @@ _WORKSPACES: dict = {}
 
 
 def _cached_workspace(device: torch.device, nbytes: int) -> Optional[torch.Tensor]:
-    """The decode kernel's split-K workspace, one per device, grown on demand.
-    It starts zero-filled and every call leaves its arrival counters at zero,
-    so calls ordered on one stream can share it."""
+    """The decode kernel's split-K workspace, one per (device, stream), grown
+    on demand.  It starts zero-filled and every call leaves its arrival
+    counters at zero, so calls ordered on one stream can share it; calls on
+    different streams, which may overlap, get different workspaces."""
     if nbytes == 0:
         return None
-    key = (device.type, device.index if device.index is not None else torch.cuda.current_device())
+    key = (device.type, device.index if device.index is not None else torch.cuda.current_device(),
+           stream_ptr(device))
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
