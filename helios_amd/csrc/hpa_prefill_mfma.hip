@@ -151,10 +151,23 @@ __device__ __forceinline__ int item_cost(const PrefillArgs& a, int item, int uni
   return ((lim + 31) >> 5) + 1;
 }
 
-// 4 x b16 transposed across each 16-lane group (see the layout above)
-__device__ __forceinline__ u32x2 lds_read_tr(const uint8_t* p) {
-  const i16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(p));
-  return __builtin_bit_cast(u32x2, r);
+// 4 x b16 transposed across each 16-lane group (see the layout above),
+// issued through inline asm.  With the builtin, the compiler's wait pass
+// cannot tell the read from the global->LDS copies still in flight and puts
+// a vmcnt(0) before it, which drains every copy issued ahead; the copies are
+// ordered by the kernel's own per-wave vmcnt waits and the step barrier
+// instead.  The compiler does not track the asm's result, so the step waits
+// for its reads with an explicit lgkmcnt(0) before any use of them.
+template <int OFF>
+__device__ __forceinline__ u32x2 lds_read_tr(uint32_t lds_addr) {
+  u32x2 r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(lds_addr), "i"(OFF));
+  return r;
+}
+
+// LDS address of a pointer into the kernel's shared array
+__device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)p;
 }
 
 // x combined with the value of lane l ^ 32 (the other half of the same row)
@@ -190,7 +203,8 @@ __global__ __launch_bounds__(64 * kPfWaves, 2) void prefill_mfma_kernel(const Pr
   constexpr int NS = QUANT ? 6 : kPfStages;
   constexpr int SSZ = QUANT ? (int)sizeof(typename ST::storage) : 4;
   static_assert(D == 64 || D == 128, "head_dim 64 or 128");
-  static_assert(kPfStages >= 3 && kPfStages <= 5, "waits below cover up to three later steps in flight");
+  static_assert(kPfStages >= 3 && (kPfStages - 2) * IPW <= 15 && (!QUANT || (NS - 2) * G8 <= 15),
+                "the copy waits below fit vmcnt's low four bits");
   // fp pools: NS stages of [K tile | V tile].  int8 pools: two dequantised
   // [K tile | V tile] buffers, then NS int8 stages of 4 wave regions.
   constexpr int SMEM = QUANT ? 2 * 2 * TILEB + NS * 4 * R8 : NS * 2 * TILEB;
@@ -283,7 +297,9 @@ __global__ __launch_bounds__(64 * kPfWaves, 2) void prefill_mfma_kernel(const Pr
   if (nsteps > 0) win.fill(trow, a.table_stride, 0);
   auto issue_loads = [&](int step, int stage) {
     const int key0 = step * 32 + 16 * half;
-    int valid = min(max(ctx - key0, 0), 16);     // rows past the context read as zeros
+    // rows past the context read as zeros; a step past the last one issues
+    // empty copies, so every step has the same loads in flight
+    int valid = step < nsteps ? min(max(ctx - key0, 0), 16) : 0;
     int phys = 0;
     if (valid > 0) {
       const int lb = key0 >> a.bs_log2;
@@ -391,29 +407,11 @@ __global__ __launch_bounds__(64 * kPfWaves, 2) void prefill_mfma_kernel(const Pr
     if constexpr (QUANT) {
       // this wave's copies for step i + 1 (dequantised below) have landed
       // once at most the later steps' groups (G8 loads each) are in flight
-      const int later = min(nsteps - 2 - i, NS - 3);
-      if (later >= 3) {
-        __builtin_amdgcn_s_waitcnt(0x0F70 | (3 * G8));
-      } else if (later == 2) {
-        __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * G8));
-      } else if (later == 1) {
-        __builtin_amdgcn_s_waitcnt(0x0F70 | G8);
-      } else {
-        __builtin_amdgcn_s_waitcnt(0x0F70);
-      }
+      __builtin_amdgcn_s_waitcnt(0x0F70 | ((NS - 3) * G8));
     } else {
       // this wave's copies for step i have landed once at most the later
       // steps' groups (IPW loads each) are still in flight
-      const int later = min(nsteps - 1 - i, kPfStages - 2);
-      if (later >= 3) {
-        __builtin_amdgcn_s_waitcnt(0x0F70 | (3 * IPW));  // vmcnt(3 IPW)
-      } else if (later == 2) {
-        __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * IPW));  // vmcnt(2 IPW)
-      } else if (later == 1) {
-        __builtin_amdgcn_s_waitcnt(0x0F70 | IPW);        // vmcnt(IPW)
-      } else {
-        __builtin_amdgcn_s_waitcnt(0x0F70);              // vmcnt(0)
-      }
+      __builtin_amdgcn_s_waitcnt(0x0F70 | ((kPfStages - 2) * IPW));
     }
     // After the barrier every wave's copies for step i are in LDS (each
     // waited for its own above) and every wave has consumed its reads of
@@ -426,7 +424,7 @@ __global__ __launch_bounds__(64 * kPfWaves, 2) void prefill_mfma_kernel(const Pr
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     // int8: the barrier also published the tile of step i (dequantised in
     // step i - 1) and retired every read of the tile step i + 1 reuses
-    if (i + NS - 1 < nsteps) issue_loads(i + NS - 1, (STAGE + NS - 1) % NS);
+    issue_loads(i + NS - 1, (STAGE + NS - 1) % NS);
     if constexpr (QUANT) {
       if (i + 1 < nsteps) dequant(i + 1, (STAGE + 1) % NS);
     }
@@ -439,15 +437,15 @@ __global__ __launch_bounds__(64 * kPfWaves, 2) void prefill_mfma_kernel(const Pr
 #pragma unroll
     for (int c = 0; c < KCH; ++c) st = M::mma(*reinterpret_cast<const u32x4*>(st_base + koff[c]), qf[c], st);
     // ---- V^T operands: dims 32db + l % 32, keys 8(2kc + r) + 4(l/32) + 0..3
-    u32x4 vf[2][DB];
+    u32x2 vtr[DB][4];
+    const uint32_t st_lds = lds_addr(st_base);
 #pragma unroll
-    for (int kc = 0; kc < 2; ++kc)
-#pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        const u32x2 lo = lds_read_tr(st_base + vofs[db] + (2 * kc) * 8 * ROWB);
-        const u32x2 hi = lds_read_tr(st_base + vofs[db] + (2 * kc + 1) * 8 * ROWB);
-        vf[kc][db] = (u32x4){lo[0], lo[1], hi[0], hi[1]};
-      }
+    for (int db = 0; db < DB; ++db) {
+      vtr[db][0] = lds_read_tr<0 * 8 * ROWB>(st_lds + vofs[db]);
+      vtr[db][1] = lds_read_tr<1 * 8 * ROWB>(st_lds + vofs[db]);
+      vtr[db][2] = lds_read_tr<2 * 8 * ROWB>(st_lds + vofs[db]);
+      vtr[db][3] = lds_read_tr<3 * 8 * ROWB>(st_lds + vofs[db]);
+    }
     // ---- online softmax over the row's 32 keys (16 here, 16 in lane ^ 32);
     // only steps crossing some row's limit pay for the mask
     float x[16];
@@ -477,6 +475,19 @@ __global__ __launch_bounds__(64 * kPfWaves, 2) void prefill_mfma_kernel(const Pr
 #pragma unroll
     for (int v = 0; v < 16; ++v)
       x[v] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[v], cs, -mref));  // -inf scores give exactly 0
+    // ---- wait for this wave's V^T reads.  The asm operands pin the wait
+    // after the last exponential and ahead of every use of the read results.
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(x[15]));
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) asm volatile("" : "+v"(vtr[db][r]));
+    u32x4 vf[2][DB];
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+        vf[kc][db] = (u32x4){vtr[db][2 * kc][0], vtr[db][2 * kc][1], vtr[db][2 * kc + 1][0], vtr[db][2 * kc + 1][1]};
     // ---- O^T += V^T . P^T, two 16-key chunks
 #pragma unroll
     for (int kc = 0; kc < 2; ++kc) {
@@ -511,24 +522,12 @@ __global__ __launch_bounds__(64 * kPfWaves, 2) void prefill_mfma_kernel(const Pr
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 #pragma unroll
-  for (int u = 0; u < NS - 1; ++u)
-    if (u < nsteps) issue_loads(u, u);
+  for (int u = 0; u < NS - 1; ++u) issue_loads(u, u);
   if constexpr (QUANT) {
     // step 0's tile: this wave's copies for step 0 landed once at most the
     // later groups are in flight
     if (nsteps > 0) {
-      const int later = min(nsteps - 1, NS - 2);
-      if (later >= 4) {
-        __builtin_amdgcn_s_waitcnt(0x0F70 | (4 * G8));
-      } else if (later == 3) {
-        __builtin_amdgcn_s_waitcnt(0x0F70 | (3 * G8));
-      } else if (later == 2) {
-        __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * G8));
-      } else if (later == 1) {
-        __builtin_amdgcn_s_waitcnt(0x0F70 | G8);
-      } else {
-        __builtin_amdgcn_s_waitcnt(0x0F70);
-      }
+      __builtin_amdgcn_s_waitcnt(0x0F70 | ((NS - 2) * G8));
       dequant(0, 0);
     }
   }
@@ -537,6 +536,9 @@ __global__ __launch_bounds__(64 * kPfWaves, 2) void prefill_mfma_kernel(const Pr
     for (int u = 0; u < NS; ++u)
       if (i0 + u < nsteps) step(i0 + u, u);
   }
+  // the empty copies issued past the last step still write LDS: they land
+  // before the workgroup ends
+  __builtin_amdgcn_s_waitcnt(0x0F70);
 
   // ---- epilogue: O = O^T / l; o[db][v] is dim 32db + 8(v/4) + 4h + v%4 of
   // row n, so every 4 consecutive values are 4 consecutive dims
