@@ -1,6 +1,7 @@
 // C-ABI of the paged decode / speculative-verify attention (the kernels and
 // their work decomposition are in hpa_decode_impl.h).
 #include "hpa_decode_impl.h"
+#include "hpa_prefill.h"
 
 namespace hpa {
 
@@ -88,6 +89,35 @@ extern "C" int hpa_paged_decode(const void* q, void* out, int q_dtype, const voi
   if (!nt)
     return fail(HPA_ERR_UNSUPPORTED,
                 "hpa_paged_decode: %d query rows per KV head exceed 64; use hpa_paged_prefill", rows);
+  if (nt == 4) {
+    // 33-64 rows per KV head: the decode kernel's four row tiles spill
+    // registers, and the MFMA prefill kernel (one 128-row tile per sequence
+    // and KV head) runs these verifies several times faster.  It takes fp16 /
+    // bf16 queries, head_dim 64 / 128 and block_size >= 16; other shapes keep
+    // the decode kernel.  No workspace is used.
+    PrefillArgs pa;
+    pa.q = q;
+    pa.out = out;
+    pa.k = k_pool;
+    pa.v = v_pool;
+    pa.ks = k_scale;
+    pa.vs = v_scale;
+    pa.tables = block_tables;
+    pa.table_stride = table_stride;
+    pa.cu_q = nullptr;
+    pa.q_pos = nullptr;
+    pa.ctx_lens = context_lens;
+    pa.num_seqs = num_seqs;
+    pa.num_q_heads = num_q_heads;
+    pa.num_kv_heads = num_kv_heads;
+    pa.group = group;
+    pa.bs_log2 = bsl;
+    pa.num_blocks = num_blocks;
+    pa.scale_log2 = sm_scale * 1.4426950408889634f;
+    pa.uniform_q = q_per_seq;
+    if (launch_prefill_mfma(pa, q_dtype, kv_dtype, scale_dtype, head_dim, q_per_seq, stream))
+      return check_launch("hpa_paged_decode");
+  }
   DecodeFn fn = pick_decode(q_dtype, kv_dtype, scale_dtype, head_dim, nt);
   if (!fn)
     return fail(HPA_ERR_UNSUPPORTED, "hpa_paged_decode: no kernel for q dtype %d, kv dtype %d, scale dtype %d, head_dim %d",

@@ -22,6 +22,11 @@ struct PrefillArgs {
   int num_seqs, num_q_heads, num_kv_heads, group;
   int bs_log2, num_blocks;
   float scale_log2;
+  // > 0: a speculative verify, uniform_q query tokens per sequence.  cu_q and
+  // q_pos are not read: sequence b's tokens are [b uniform_q, (b + 1)
+  // uniform_q) and its first token sits at ctx_lens[b] - uniform_q.
+  // Honoured by the MFMA kernel only.
+  int uniform_q;
 };
 
 // LDS-tiled 32x32 MFMA prefill for fp16 / bf16 queries over pools of the

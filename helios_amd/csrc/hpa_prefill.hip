@@ -192,6 +192,7 @@ extern "C" int hpa_paged_prefill(const void* q, void* out, int q_dtype, const vo
   a.bs_log2 = bsl;
   a.num_blocks = num_blocks;
   a.scale_log2 = sm_scale * 1.4426950408889634f;
+  a.uniform_q = 0;
   if (launch_prefill_mfma(a, q_dtype, kv_dtype, scale_dtype, head_dim, max_q_len, stream))
     return check_launch("hpa_paged_prefill");
   const long rows = (long)max_q_len * a.group;

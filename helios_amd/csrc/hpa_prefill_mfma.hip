@@ -4,7 +4,9 @@
 // Same contract as prefill_kernel (hpa_prefill.hip): sequence b owns query
 // tokens [cu_q[b], cu_q[b+1]); its token i sits at position q_pos[b] + i and
 // attends keys [0, min(q_pos[b] + i + 1, ctx[b])) -- helios' causal rule
-// (reference exec/paged_attn.py:401-404).
+// (reference exec/paged_attn.py:401-404).  A verify launch (uniform_q > 0,
+// from hpa_paged_decode) gives every sequence uniform_q tokens ending at
+// ctx[b] - 1 and reads neither cu_q nor q_pos.
 //
 // A workgroup of four waves owns 128 consecutive (token, head-in-group) rows
 // of one (sequence, KV head); each wave owns 32 of them, one 32x32 MFMA tile.
@@ -141,13 +143,24 @@ constexpr int kPfLptMax = 512;           // items per XCD up to which workgroups
 // 8j + x, so each XCD schedules its own items longest-first (list
 // scheduling's LPT rule) and a unit's tiles stay on one XCD's L2 whenever the
 // unit count is a multiple of 8.  Returns steps + 1, or 0 for an empty tile.
+// sequence b's query tokens [q0, q0 + qn), the first at position pos0
+struct SeqSpan {
+  int q0, qn, pos0;
+};
+__device__ __forceinline__ SeqSpan seq_span(const PrefillArgs& a, int b) {
+  if (a.uniform_q > 0) return {b * a.uniform_q, a.uniform_q, a.ctx_lens[b] - a.uniform_q};
+  const int q0 = a.cu_q[b];
+  return {q0, a.cu_q[b + 1] - q0, a.q_pos[b]};
+}
+
 __device__ __forceinline__ int item_cost(const PrefillArgs& a, int item, int units, int tiles) {
   const int unit = item % units, tile = tiles - 1 - item / units;
   const int b = unit / a.num_kv_heads;
-  const int rows = (a.cu_q[b + 1] - a.cu_q[b]) * a.group;
+  const SeqSpan sp = seq_span(a, b);
+  const int rows = sp.qn * a.group;
   if (tile * kPfRows >= rows) return 0;
   const int rlast = min(tile * kPfRows + kPfRows - 1, rows - 1);
-  const int lim = max(min(a.q_pos[b] + rlast / a.group + 1, a.ctx_lens[b]), 0);
+  const int lim = max(min(sp.pos0 + rlast / a.group + 1, a.ctx_lens[b]), 0);
   return ((lim + 31) >> 5) + 1;
 }
 
@@ -240,11 +253,12 @@ __global__ __launch_bounds__(64 * kPfWaves, 2) void prefill_mfma_kernel(const Pr
   const int tile = tiles_per_unit - 1 - item / units;
   const int b = unit / a.num_kv_heads, kvh = unit - b * a.num_kv_heads;
   const int G = a.group;
-  const int q0 = a.cu_q[b];
-  const int rows = (a.cu_q[b + 1] - q0) * G;
+  const SeqSpan sp = seq_span(a, b);
+  const int q0 = sp.q0;
+  const int rows = sp.qn * G;
   if (tile * kPfRows >= rows) return;  // uniform over the workgroup, before any barrier
   const int ctx = a.ctx_lens[b];
-  const int pos0 = a.q_pos[b];
+  const int pos0 = sp.pos0;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int h = lane >> 5, n = lane & 31;

@@ -77,7 +77,10 @@ size_t hpa_decode_workspace_size(int num_seqs, int q_per_seq, int num_q_heads, i
  * (helios' causal rule, paged_attn.py:401-404, with start_pos = context -
  * q_per_seq).  An empty context yields zeros.  Softmax scale sm_scale.
  * The query rows of one KV head ((num_q_heads / num_kv_heads) * q_per_seq)
- * must not exceed 64; use hpa_paged_prefill beyond that.
+ * must not exceed 64; use hpa_paged_prefill beyond that.  33 to 64 rows run
+ * on the MFMA prefill kernel when it takes the shape (fp16 / bf16 queries,
+ * head_dim 64 or 128, block_size >= 16), with the same results as
+ * hpa_paged_prefill over the same tokens; the workspace is then unused.
  * part_tokens: smallest share of the context, in tokens, one wave streams
  * (0 = library default); it changes only the summation order.
  * workspace: at least hpa_decode_workspace_size(...) bytes of device memory

@@ -22,6 +22,7 @@ from helios_amd import (
     paged_attention_decode,
     paged_attention_decode_batched,
     paged_attention_decode_hip,
+    paged_attention_varlen,
     paged_attention_verify_batched,
 )
 from oracle import paged_ref as R
@@ -175,6 +176,34 @@ def test_verify_rows_and_gqa_groups(Hq, Hkv, T, quant):
     got = paged_attention_verify_batched(q, cache, tables, lens, T)
     want = _oracle_decode(cache, q, tables, lens, q_per_seq=T)
     _check(got, want, torch.float16, f"verify {Hq}/{Hkv}x{T}")
+
+
+@pytest.mark.parametrize("quant", [False, True])
+@pytest.mark.parametrize("Hq,Hkv,T", [(32, 4, 8), (16, 4, 9), (8, 1, 5)])
+def test_wide_verify_runs_the_mfma_prefill_kernel(Hq, Hkv, T, quant):
+    """33-64 query rows per KV head go to the MFMA prefill kernel: the
+    verify equals, bit for bit, the same tokens through paged_attention_varlen
+    (start = context - T), and the oracle."""
+    print(f"wide verify {Hq}/{Hkv}x{T} int8 {quant}", flush=True)
+    lens = [T, T + 5, 40, 129, 300]
+    cache, tables, q = _case(80 + Hq + T, len(lens), lens, Hq, Hkv, 128, 16, torch.float16,
+                             quant=quant, q_per_seq=T)
+    got = paged_attention_verify_batched(q, cache, tables, lens, T)
+    same = paged_attention_varlen(q, cache, tables, [T] * len(lens), [c - T for c in lens], lens)
+    assert torch.equal(got, same)
+    _check(got, _oracle_decode(cache, q, tables, lens, q_per_seq=T), torch.float16, "wide verify")
+
+
+@pytest.mark.parametrize("D,bs,dtype", [(128, 8, torch.float16), (32, 16, torch.float16),
+                                        (64, 16, torch.float32)])
+def test_wide_verify_on_shapes_the_mfma_kernel_does_not_take(D, bs, dtype):
+    """33-64 rows per KV head with block size 8, head_dim 32 or fp32 queries
+    stay on the decode kernel (four row tiles)."""
+    print(f"wide verify on the decode kernel: D {D}, block {bs}, {dtype}", flush=True)
+    T, lens = 5, [5, 12, 40, 129, 300]
+    cache, tables, q = _case(90 + D + bs, len(lens), lens, 8, 1, D, bs, dtype, q_per_seq=T)
+    got = paged_attention_verify_batched(q, cache, tables, lens, T)
+    _check(got, _oracle_decode(cache, q, tables, lens, q_per_seq=T), dtype, f"decode-kernel verify D={D}")
 
 
 @pytest.mark.parametrize("part", [128, 256, 512])
