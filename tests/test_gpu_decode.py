@@ -26,7 +26,7 @@ from helios_amd import (
     paged_attention_verify_batched,
 )
 from oracle import paged_ref as R
-from tests.gpu_util import dev, fill_cache, max_abs, pool_of, ragged_tables, to_np
+from tests.gpu_util import dev, fill_cache, max_abs, pool_dequantized, pool_of, ragged_tables, to_np
 
 pytestmark = pytest.mark.gpu
 
@@ -179,19 +179,25 @@ def test_verify_rows_and_gqa_groups(Hq, Hkv, T, quant):
 
 
 @pytest.mark.parametrize("quant", [False, True])
-@pytest.mark.parametrize("Hq,Hkv,T", [(32, 4, 8), (16, 4, 9), (8, 1, 5)])
-def test_wide_verify_runs_the_mfma_prefill_kernel(Hq, Hkv, T, quant):
+@pytest.mark.parametrize("Hq,Hkv,T,D,dtype", [(32, 4, 8, 128, torch.float16), (16, 4, 9, 128, torch.float16),
+                                              (8, 1, 5, 128, torch.float16), (8, 1, 6, 64, torch.bfloat16)])
+def test_wide_verify_runs_the_mfma_prefill_kernel(Hq, Hkv, T, D, dtype, quant):
     """33-64 query rows per KV head go to the MFMA prefill kernel: the
     verify equals, bit for bit, the same tokens through paged_attention_varlen
-    (start = context - T), and the oracle."""
-    print(f"wide verify {Hq}/{Hkv}x{T} int8 {quant}", flush=True)
+    (start = context - T), and the oracle.  On int8 pools that kernel attends
+    over the dequantised values rounded to the compute dtype, as helios'
+    gather hands them over (paged_attn.py:213-235), so the oracle reads the
+    same values."""
+    print(f"wide verify {Hq}/{Hkv}x{T} D {D} {dtype} int8 {quant}", flush=True)
     lens = [T, T + 5, 40, 129, 300]
-    cache, tables, q = _case(80 + Hq + T, len(lens), lens, Hq, Hkv, 128, 16, torch.float16,
+    cache, tables, q = _case(80 + Hq + T, len(lens), lens, Hq, Hkv, D, 16, dtype,
                              quant=quant, q_per_seq=T)
     got = paged_attention_verify_batched(q, cache, tables, lens, T)
     same = paged_attention_varlen(q, cache, tables, [T] * len(lens), [c - T for c in lens], lens)
     assert torch.equal(got, same)
-    _check(got, _oracle_decode(cache, q, tables, lens, q_per_seq=T), torch.float16, "wide verify")
+    pool = pool_dequantized(cache) if quant else pool_of(cache)
+    want = R.paged_verify_batched(to_np(q).astype(np.float32), pool, tables, lens, T)
+    _check(got, want, dtype, "wide verify")
 
 
 @pytest.mark.parametrize("D,bs,dtype", [(128, 8, torch.float16), (32, 16, torch.float16),
