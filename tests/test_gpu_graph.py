@@ -7,7 +7,8 @@ and replayed.  The decode kernel's split-K counters are returned to zero by
 the kernel itself, so a replay needs no memset node.  Each replay here runs
 after eager work and a synchronisation, with new inputs copied into the
 captured tensors, and must equal the same calls made eagerly on twin caches,
-bit for bit."""
+bit for bit.  Nine query tokens per sequence (36 rows per KV head) run the
+verify on the MFMA prefill kernel."""
 
 from __future__ import annotations
 
@@ -20,7 +21,7 @@ from tests.test_step_meta import Sim
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("quant,q_per_seq", [(False, 1), (True, 1), (True, 3)])
+@pytest.mark.parametrize("quant,q_per_seq", [(False, 1), (True, 1), (True, 3), (False, 9), (True, 9)])
 def test_captured_step_replays_equal_eager(quant, q_per_seq):
     print(f"graph replay: int8 {quant}, q_per_seq {q_per_seq}", flush=True)
     gen = torch.Generator(device="cuda").manual_seed(5)
