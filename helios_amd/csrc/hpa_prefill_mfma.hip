@@ -489,8 +489,10 @@ __global__ __launch_bounds__(64 * kPfWaves, 2) void prefill_mfma_kernel(const Pr
 #pragma unroll
     for (int v = 0; v < 16; ++v)
       x[v] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[v], cs, -mref));  // -inf scores give exactly 0
-    // ---- wait for this wave's V^T reads.  The asm operands pin the wait
-    // after the last exponential and ahead of every use of the read results.
+    // ---- wait for this wave's V^T reads.  The asm operands keep the wait
+    // ahead of every use of the read results (the empty asms below) and
+    // after the exponential of x[15], so the reads' latency overlaps the
+    // softmax.
     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(x[15]));
 #pragma unroll
     for (int db = 0; db < DB; ++db)
