@@ -90,7 +90,7 @@ def _fill_by_writes(cache, lens, tables_t, gen, device, chunk_tokens=1 << 19):
 class DecodeWorkload(Workload):
     """Configs 2, 3 and 5: batched decode (q_per_seq 1) or verify (3)."""
 
-    def __init__(self, cfg, device, seed, part_tokens=0, copies=1):
+    def __init__(self, cfg, device, seed, part_tokens=0, copies=1, scale_dtype=None):
         import numpy as np
         import torch
 
@@ -124,10 +124,11 @@ class DecodeWorkload(Workload):
         # Configs 2/3 fit in the 256 MB Infinity Cache: rotate over enough
         # pool copies that every step reads from HBM.
         self.caches = []
+        self.scale_dtype = scale_dtype or torch.float16
         for _ in range(copies):
             if quant:
                 c = H.QuantizedPagedKVCache(nb, BLOCK, Hkv, D, dtype=dtype, device=device,
-                                            scale_dtype=torch.float16)
+                                            scale_dtype=self.scale_dtype)
             else:
                 c = H.PagedKVCache(nb, BLOCK, Hkv, D, dtype=dtype, device=device)
             _fill_by_writes(c, lens, self.tables_t, gen, device)
@@ -142,14 +143,15 @@ class DecodeWorkload(Workload):
             self.new_pos = torch.tensor([c - 1 for c in lens], dtype=torch.int32, device=device)
             self.new_cu = torch.arange(0, B + 1, dtype=torch.int32, device=device)
         self.i = 0
-        kvb = D * (1 if quant else (4 if cfg == 1 else 2)) + (2 if quant else 0)
+        sb = 4 if self.scale_dtype == torch.float32 else 2
+        kvb = D * (1 if quant else (4 if cfg == 1 else 2)) + (sb if quant else 0)
         elt = 4 if cfg == 1 else 2
         sum_ctx = sum(lens)
         n_tab = sum((c + BLOCK - 1) // BLOCK for c in lens)
         self.kv_bytes = sum_ctx * 2 * Hkv * kvb
         self.alg_bytes = self.kv_bytes + 2 * B * Tq * Hq * D * elt + 4 * n_tab + 4 * B
-        if cfg == 3:  # the write: read K,V fp16, write int8 + fp16 scale
-            self.alg_bytes += B * 2 * Hkv * (D * 2 + D + 2)
+        if cfg == 3:  # the write: read K,V fp16, write int8 + scale
+            self.alg_bytes += B * 2 * Hkv * (D * 2 + D + sb)
         self.flops = 4 * D * Hq * sum(sum(min(c, c - Tq + t + 1) for t in range(Tq)) for c in lens)
         self.tokens = B * Tq
 
@@ -162,18 +164,20 @@ class DecodeWorkload(Workload):
             H.write_kv(c, self.tables_t, self.new_pos, self.new_k, self.new_v,
                        cu_query_lens=self.new_cu, max_query_len=1)
         ks, vs = c._scales()
-        H.paged_attention_decode_hip(
+        return H.paged_attention_decode_hip(
             self.q, c.k_cache, c.v_cache, self.tables_t, self.lens_t, self.scale, ks, vs,
             q_per_seq=self.Tq, max_context_len=self.max_ctx, part_tokens=self.part_tokens,
             out=self.out, workspace=self.ws,
         )
 
     def config(self):
+        import torch
+
         return {"workload": self.name, "batch": self.B, "q_per_seq": self.Tq,
                 "n_q_heads": self.Hq, "n_kv_heads": self.Hkv, "head_dim": self.D,
                 "block_size": BLOCK, "kv_dtype": "int8" if self.quant else
                 ("fp32" if self.cfg == 1 else "fp16"),
-                "scale_dtype": "fp16" if self.quant else None,
+                "scale_dtype": ("fp32" if self.scale_dtype == torch.float32 else "fp16") if self.quant else None,
                 "context": {"mean": round(sum(self.lens) / len(self.lens), 1),
                             "max": self.max_ctx, "min": min(self.lens)},
                 "pool_copies": len(self.caches), "part_tokens": self.part_tokens or "auto"}
@@ -279,13 +283,14 @@ class PrefillWorkload(Workload):
         kvb = D + 2 if kv_int8 else 2 * D
         self.alg_bytes = sum(ctxs) * 2 * Hkv * kvb + 2 * B * T * Hq * D * 2 + 4 * n_tab
         self.tokens = B * T
+        self.out = torch.empty_like(self.q)
 
     def step(self):
         import helios_amd as H
 
-        H.paged_attention_varlen(self.q, self.cache, self.tables_t, self.qlens, self.pos_t,
-                                 self.ctx_t, self.scale, max_query_len=self.T,
-                                 cu_query_lens=self.cu)
+        return H.paged_attention_varlen(self.q, self.cache, self.tables_t, self.qlens, self.pos_t,
+                                        self.ctx_t, self.scale, max_query_len=self.T,
+                                        cu_query_lens=self.cu, out=self.out)
 
     def config(self):
         return {"workload": self.name, "sequences": self.B, "chunk": self.T,
@@ -318,16 +323,77 @@ class PrefillWorkload(Workload):
         return done * self.T, dt, f"{done} of {self.B} sequences ({done * self.T} query tokens)"
 
 
-def _cpu_threads():
+def _cpu_model():
     try:
-        from threadpoolctl import threadpool_info
-
-        n = [i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"]
-        if n:
-            return int(max(n))
-    except Exception:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
         pass
-    return len(os.sched_getaffinity(0))
+    return None
+
+
+def cpu_baseline(wl, budget_s):
+    """The oracle's restatement of helios' CPU route on a bounded sample,
+    with every core this process may run on (BASELINE.md's rule: n =
+    len(sched_getaffinity)) given to the BLAS pool."""
+    n = len(os.sched_getaffinity(0))
+    try:
+        from threadpoolctl import threadpool_limits
+
+        with threadpool_limits(limits=n, user_api="blas"):
+            tokens, secs, sample = wl.cpu_baseline(budget_s)
+    except ImportError:
+        tokens, secs, sample = wl.cpu_baseline(budget_s)
+    return {"value": round(tokens / secs, 1) if secs > 0 else None, "unit": "tokens/s",
+            "cores": n, "cpu_model": _cpu_model(), "kind": "port", "sample": sample,
+            "seconds": round(secs, 2)}
+
+
+def time_steps(wl, steps, warmup, warmup_s):
+    """`warmup` untimed steps, continued until at least `warmup_s` seconds
+    have passed (the GPU clock needs tens of milliseconds of sustained work
+    to ramp up), then exactly `steps` timed steps, each bracketed by its own
+    pair of HIP events on the stream the kernels run on (torch's current
+    stream).  Returns (median ms, mean ms, warmup steps run, seconds of the
+    timed region by the host clock)."""
+    import torch
+
+    stream = torch.cuda.current_stream()
+    done, t0 = 0, time.perf_counter()
+    while done < warmup or time.perf_counter() - t0 < warmup_s:
+        wl.step()
+        done += 1
+        if done % 50 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    t_wall = time.perf_counter()
+    for e0, e1 in ev:
+        e0.record(stream)
+        wl.step()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_wall
+    ms = sorted(e0.elapsed_time(e1) for e0, e1 in ev)
+    med = ms[len(ms) // 2] if len(ms) % 2 else 0.5 * (ms[len(ms) // 2 - 1] + ms[len(ms) // 2])
+    return med, sum(ms) / len(ms), done, wall
+
+
+def roofline(wl, ms, key):
+    if wl.bound == "hbm":
+        achieved = wl.alg_bytes / (ms * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": _traffic(key), "algorithmic_bytes": int(wl.alg_bytes)}
+    else:
+        achieved = wl.flops / (ms * 1e-3) / 1e12
+        roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_F16_PEAK_TFS,
+                "unit": "TFLOP/s", "frac": round(achieved / MFMA_F16_PEAK_TFS, 4),
+                "traffic": _traffic(key), "algorithmic_flops": int(wl.flops)}
+    roof["kernel"] = "decode_kernel" if wl.bound == "hbm" else "prefill_mfma_kernel"
+    return roof
 
 
 def _traffic(workload_key):
@@ -576,9 +642,7 @@ def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    # the GPU clock takes tens of milliseconds of sustained work to ramp up;
-    # a short warmup understates the steady-state rate by up to ~20%
-    ap.add_argument("--warmup", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", type=int, default=5, choices=[1, 2, 3, 4, 5])
     ap.add_argument("--seed", type=int, default=None)
     ap.add_argument("--kv-int8", action="store_true",
@@ -587,8 +651,12 @@ def main():
                     help="split-K partition size for decode (0 = library default)")
     ap.add_argument("--copies", type=int, default=None,
                     help="pool copies rotated per step (default: enough to exceed 256 MB)")
+    ap.add_argument("--warmup-s", type=float, default=1.0,
+                    help="untimed warmup continues until this many seconds have passed")
     ap.add_argument("--cpu-budget", type=float, default=15.0,
                     help="seconds of CPU baseline work (0 disables it)")
+    ap.add_argument("--no-prefill", action="store_true",
+                    help="config 5 only: skip the config-4 prefill measured beside it")
     ap.add_argument("--meta-layers", type=int, default=0, metavar="L",
                     help="only time a decode-verify step over L layers with device-resident "
                          "vs per-layer list metadata, print its own JSON line, and exit")
@@ -648,42 +716,12 @@ def main():
             copies = 1 if args.config in (1, 5) else 5
         wl = DecodeWorkload(args.config, device, seed, args.part_tokens, copies)
 
-    for _ in range(args.warmup):
-        wl.step()
-    torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    t_wall = time.perf_counter()
-    start.record()
-    for _ in range(args.steps):
-        wl.step()
-    end.record()
-    end.synchronize()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t_wall
-    ms = start.elapsed_time(end) / args.steps
-
-    value = wl.tokens / (ms * 1e-3)
-    if wl.bound == "hbm":
-        achieved = wl.alg_bytes / (ms * 1e-3) / 1e9
-        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                "traffic": _traffic(f"config{args.config}" + ("_int8" if args.kv_int8 else "")),
-                "algorithmic_bytes": int(wl.alg_bytes)}
-    else:
-        achieved = wl.flops / (ms * 1e-3) / 1e12
-        roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_F16_PEAK_TFS,
-                "unit": "TFLOP/s", "frac": round(achieved / MFMA_F16_PEAK_TFS, 4),
-                "traffic": _traffic(f"config{args.config}" + ("_int8" if args.kv_int8 else "")),
-                "algorithmic_flops": int(wl.flops)}
-    roof["kernel"] = "decode_kernel" if wl.bound == "hbm" else "prefill_mfma_kernel"
-
-    cpu = None
-    if args.cpu_budget > 0:
-        tokens, secs, sample = wl.cpu_baseline(args.cpu_budget)
-        cpu = {"value": round(tokens / secs, 1) if secs > 0 else None, "unit": "tokens/s",
-               "cores": _cpu_threads(), "kind": "port", "sample": sample,
-               "seconds": round(secs, 2)}
+    print(f"bench: {wl.name} built; timing {args.steps} steps", file=sys.stderr, flush=True)
+    med, mean, warm_done, wall = time_steps(wl, args.steps, args.warmup, args.warmup_s)
+    print(f"bench: {med * 1e3:.1f} us per step (median); CPU baseline next", file=sys.stderr, flush=True)
+    key = f"config{args.config}" + ("_int8" if args.kv_int8 else "")
+    value = wl.tokens / (med * 1e-3)
+    cpu = cpu_baseline(wl, args.cpu_budget) if args.cpu_budget > 0 else None
 
     line = {
         "metric": "paged-attn decode tokens/s + achieved HBM GB/s (% peak) on 1 MI355X"
@@ -693,7 +731,11 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms, 5),
+        "warmup_s": args.warmup_s,
+        "warmup_steps_run": warm_done,
+        "ms_per_step": round(med, 5),
+        "ms_per_step_mean": round(mean, 5),
+        "timing": "median of per-step HIP event pairs on the kernels' stream",
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -701,10 +743,24 @@ def main():
         ("f32" if args.config == 1 else "f16"),
         "data": "synthetic (seeded N(0,1); int8 KV quantized on the GPU by the library's write kernel)",
         "config": wl.config(),
-        "roofline": roof,
+        "roofline": roofline(wl, med, key),
         "cpu_baseline": cpu,
         "wall_s_timed_region": round(wall, 4),
     }
+    if args.config == 5 and not args.no_prefill:
+        # config 4 (the MFMA-bound chunked prefill) measured in the same run
+        pw = PrefillWorkload(device, 3)
+        print(f"bench: {pw.name} built; timing {args.steps} steps", file=sys.stderr, flush=True)
+        pmed, pmean, pwarm, _ = time_steps(pw, args.steps, args.warmup, args.warmup_s)
+        print(f"bench: {pmed * 1e3:.1f} us per step (median); CPU baseline next", file=sys.stderr, flush=True)
+        line["prefill"] = {
+            "metric": "paged-attn chunked-prefill tokens/s + MFMA TFLOP/s (% peak) on 1 MI355X",
+            "value": round(pw.tokens / (pmed * 1e-3), 1), "unit": "tokens/s",
+            "ms_per_step": round(pmed, 5), "ms_per_step_mean": round(pmean, 5),
+            "warmup_steps_run": pwarm, "dtype": "f16", "config": pw.config(),
+            "roofline": roofline(pw, pmed, "config4"),
+            "cpu_baseline": cpu_baseline(pw, args.cpu_budget) if args.cpu_budget > 0 else None,
+        }
     print(json.dumps(line))
 
 

@@ -13,6 +13,7 @@ from .paged_attn import (  # noqa: F401
     _repeat_kv,
     _repeat_kv_batched,
     copy_blocks,
+    decode_workspace,
     decode_workspace_bytes,
     hip_available,
     paged_attention_decode,
@@ -21,6 +22,7 @@ from .paged_attn import (  # noqa: F401
     paged_attention_prefill,
     paged_attention_varlen,
     paged_attention_verify_batched,
+    reset_decode_workspace,
     write_kv,
 )
 from .step_meta import DeviceAttnMeta, DeviceBlockTables, batched_attention, write_kv_batched  # noqa: F401
@@ -29,6 +31,7 @@ __all__ = [
     "PagedKVCache",
     "QuantizedPagedKVCache",
     "copy_blocks",
+    "decode_workspace",
     "decode_workspace_bytes",
     "hip_available",
     "paged_attention_decode",
@@ -37,6 +40,7 @@ __all__ = [
     "paged_attention_prefill",
     "paged_attention_varlen",
     "paged_attention_verify_batched",
+    "reset_decode_workspace",
     "write_kv",
     "DeviceAttnMeta",
     "DeviceBlockTables",

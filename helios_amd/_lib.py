@@ -56,7 +56,7 @@ SIGNATURES = {
         _c_int,
         [_c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_int,
          _c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_int, _c_int, _c_int,
-         _c_int, _c_int, _c_int, _c_float, _c_ptr],
+         _c_int, _c_int, _c_int, _c_int, _c_float, _c_ptr],
     ),
     "hpa_kv_write": (
         _c_int,

@@ -57,7 +57,8 @@ def _compile(src: Path) -> Path:
 def build(verbose: bool = False) -> Path:
     """Compile every kernel source and link the shared library."""
     OBJ_DIR.mkdir(exist_ok=True)
-    sources = sorted(CSRC.glob("*.hip"))
+    # the decode kernel tables take longest; start them first
+    sources = sorted(CSRC.glob("*.hip"), key=lambda p: ("_decode_" not in p.name, p.name))
     workers = max(1, min(len(sources), os.cpu_count() or 1, 16))
     with cf.ThreadPoolExecutor(workers) as ex:
         objs = list(ex.map(_compile, sources))

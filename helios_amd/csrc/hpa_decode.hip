@@ -18,7 +18,8 @@ static int decode_nt(int rows) { return rows <= 16 ? 1 : rows <= 32 ? 2 : rows <
 
 // Waves launched and the per-wave slice floor for these shapes.  The host
 // sees only max_context_len, so the wave count is sized on the upper bound
-// of the step count; the kernel computes the real slices.
+// of the step count; the kernel computes the real slices from the real
+// contexts (a context above max_context_len only makes the slices longer).
 struct DecodePlan {
   int waves, min_steps;
 };
@@ -26,7 +27,7 @@ static DecodePlan plan_decode(int num_seqs, int num_kv_heads, int max_context_le
   DecodePlan p;
   const int mt = min_tokens > 0 ? std::min(min_tokens, 1 << 20) : kDefaultMinTokens;
   p.min_steps = std::max(1, (mt + 31) / 32);
-  const long per_unit = std::max(1, (max_context_len + 31) / 32) + kUnitCost;
+  const long per_unit = std::max(1L, ((long)std::min(max_context_len, kMaxContext) + 31) / 32) + kUnitCost;
   const long ub = (long)num_seqs * num_kv_heads * per_unit;
   const long w = (ub + p.min_steps - 1) / p.min_steps;
   p.waves = (int)std::max(1L, std::min<long>(w, kWaveCap));
@@ -56,8 +57,9 @@ extern "C" size_t hpa_decode_workspace_size(int num_seqs, int q_per_seq, int num
   if (num_seqs <= 0 || num_kv_heads <= 0 || num_q_heads <= 0 || q_per_seq <= 0 || head_dim <= 0 ||
       num_q_heads % num_kv_heads)
     return 0;
-  const DecodePlan p = plan_decode(num_seqs, num_kv_heads, std::max(0, max_context_len), part_tokens);
   const int rows = (num_q_heads / num_kv_heads) * q_per_seq;
+  if (!decode_nt(rows)) return 0;  // more than 64 rows: the prefill kernels, no workspace
+  const DecodePlan p = plan_decode(num_seqs, num_kv_heads, std::max(0, max_context_len), part_tokens);
   return ws_bytes(p.waves, rows, head_dim);
 }
 
@@ -86,15 +88,16 @@ extern "C" int hpa_paged_decode(const void* q, void* out, int q_dtype, const voi
   const int group = num_q_heads / num_kv_heads;
   const int rows = group * q_per_seq;
   const int nt = decode_nt(rows);
-  if (!nt)
-    return fail(HPA_ERR_UNSUPPORTED,
-                "hpa_paged_decode: %d query rows per KV head exceed 64; use hpa_paged_prefill", rows);
-  if (nt == 4) {
-    // 33-64 rows per KV head: the decode kernel's four row tiles spill
-    // registers, and the MFMA prefill kernel (one 128-row tile per sequence
-    // and KV head) runs these verifies several times faster.  It takes fp16 /
-    // bf16 queries, head_dim 64 / 128 and block_size >= 16; other shapes keep
-    // the decode kernel.  No workspace is used.
+  if (nt == 0 || nt == 4) {
+    // More than 32 query rows per KV head (a wide speculative verify): the
+    // decode kernel's four row tiles spill registers and it takes at most
+    // 64 rows, while the prefill kernels tile any number of rows.  The MFMA
+    // prefill kernel (fp16 / bf16 queries, head_dim 64 / 128, block_size >=
+    // 16) runs these verifies several times faster; past 64 rows, shapes it
+    // does not take run on the generic prefill kernel.  Both compute the same
+    // causal rule as hpa_paged_prefill over the same tokens, in a mode where
+    // sequence b's tokens are [b q_per_seq, (b + 1) q_per_seq) and end at its
+    // context; no workspace is used.
     PrefillArgs pa;
     pa.q = q;
     pa.out = out;
@@ -108,6 +111,7 @@ extern "C" int hpa_paged_decode(const void* q, void* out, int q_dtype, const voi
     pa.q_pos = nullptr;
     pa.ctx_lens = context_lens;
     pa.num_seqs = num_seqs;
+    pa.num_tokens = num_seqs * q_per_seq;
     pa.num_q_heads = num_q_heads;
     pa.num_kv_heads = num_kv_heads;
     pa.group = group;
@@ -117,14 +121,16 @@ extern "C" int hpa_paged_decode(const void* q, void* out, int q_dtype, const voi
     pa.uniform_q = q_per_seq;
     if (launch_prefill_mfma(pa, q_dtype, kv_dtype, scale_dtype, head_dim, q_per_seq, stream))
       return check_launch("hpa_paged_decode");
+    if (nt == 0) {
+      const int st = launch_prefill_generic(pa, q_dtype, kv_dtype, scale_dtype, head_dim, q_per_seq, stream);
+      if (st != HPA_OK) return st;
+      return check_launch("hpa_paged_decode");
+    }
   }
   DecodeFn fn = pick_decode(q_dtype, kv_dtype, scale_dtype, head_dim, nt);
   if (!fn)
     return fail(HPA_ERR_UNSUPPORTED, "hpa_paged_decode: no kernel for q dtype %d, kv dtype %d, scale dtype %d, head_dim %d",
                 q_dtype, kv_dtype, scale_dtype, head_dim);
-  if ((long)num_seqs * num_kv_heads * (std::max(1, (max_context_len + 31) / 32)) > (long)INT32_MAX / 2)
-    return fail(HPA_ERR_UNSUPPORTED, "hpa_paged_decode: %d sequences x %d KV heads x context %d is too large",
-                num_seqs, num_kv_heads, max_context_len);
   const DecodePlan p = plan_decode(num_seqs, num_kv_heads, max_context_len, part_tokens);
   if ((long)num_seqs * num_kv_heads > kMaxUnits)
     return fail(HPA_ERR_UNSUPPORTED, "hpa_paged_decode: %d sequences x %d KV heads exceed %ld",
@@ -153,7 +159,6 @@ extern "C" int hpa_paged_decode(const void* q, void* out, int q_dtype, const voi
   a.bs_log2 = bsl;
   a.num_blocks = num_blocks;
   a.scale_log2 = sm_scale * 1.4426950408889634f;
-  a.max_ctx = max_context_len;
   a.num_waves = p.waves;
   a.min_steps = p.min_steps;
   // with one wave every unit is whole and the workspace is never touched

@@ -50,7 +50,6 @@ struct DecodeArgs {
   int num_seqs, q_per_seq, num_q_heads, num_kv_heads, group, rows;
   int bs_log2, num_blocks;
   float scale_log2;
-  int max_ctx;     // contexts are clamped here
   int num_waves;   // W: waves launched
   int min_steps;   // lower bound on a wave's slice, in 32-key steps
   int* counters;   // [num_seqs * Hkv] arrival counters, zero between calls
@@ -72,39 +71,52 @@ constexpr int kDefaultMinTokens = 256;  // per-wave slice floor (8 steps)
 // steps plus this, so waves holding many short units get fewer steps.
 constexpr int kUnitCost = 4;
 
-__device__ __forceinline__ int unit_steps(int ctx, int max_ctx) {
-  ctx = min(ctx, max_ctx);
+// Contexts are honoured as given up to 2^30 tokens (keys are int32 and a
+// step index times 32 must not overflow); the launch's max_context_len only
+// sizes the grid.  Positions in a head's step space are 64-bit sums.
+constexpr int kMaxContext = 1 << 30;
+
+__device__ __forceinline__ int clamp_ctx(int ctx) { return min(ctx, kMaxContext); }
+
+__device__ __forceinline__ int unit_steps(int ctx) {
+  ctx = clamp_ctx(ctx);
   return ctx <= 0 ? 1 : (ctx + 31) >> 5;
 }
 
-__device__ __forceinline__ int wave_sum_i(int x) {
+__device__ __forceinline__ long wave_sum_l(long x) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
   return x;
 }
 
-__device__ __forceinline__ int wave_incl_scan_i(int x) {
+__device__ __forceinline__ long wave_incl_scan_l(long x) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
-    const int y = __shfl_up(x, o);
+    const long y = __shfl_up(x, o);
     if (lane >= o) x += y;
   }
   return x;
+}
+
+__device__ __forceinline__ long uniform_l(long x) {
+  const int lo = __builtin_amdgcn_readfirstlane((int)(x & 0xffffffffL));
+  const int hi = __builtin_amdgcn_readfirstlane((int)(x >> 32));
+  return (long)(((unsigned long)(unsigned)hi << 32) | (unsigned)lo);
 }
 
 // Position of a wave in the global step range.
 struct UnitPos {
   int b, kvh;  // unit
   int n;       // its steps
-  int g;       // global position where its cost range starts
+  long g;      // global position where its cost range starts
 };
 
 // Cost (steps + kUnitCost per unit) per KV head summed over all sequences
 // (identical in every wave).
-__device__ int total_steps_per_head(const DecodeArgs& a) {
+__device__ long total_steps_per_head(const DecodeArgs& a) {
   const int lane = threadIdx.x & 63;
-  int acc = 0;
+  long acc = 0;
   for (int base = 0; base < a.num_seqs; base += 256) {
     int c[4];
 #pragma unroll
@@ -114,35 +126,35 @@ __device__ int total_steps_per_head(const DecodeArgs& a) {
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      if (base + 64 * i + lane < a.num_seqs) acc += unit_steps(c[i], a.max_ctx) + kUnitCost;
+      if (base + 64 * i + lane < a.num_seqs) acc += unit_steps(c[i]) + kUnitCost;
   }
-  return wave_sum_i(acc);
+  return wave_sum_l(acc);
 }
 
 // The sequence whose cost range in one KV head's position space holds s0
 // (< total).  A sequence's range is kUnitCost positions of overhead followed
 // by its steps.  Wave-uniform result; the caller sets the head.
-__device__ UnitPos locate(const DecodeArgs& a, int s0) {
+__device__ UnitPos locate(const DecodeArgs& a, long s0) {
   const int lane = threadIdx.x & 63;
-  int run = 0;  // positions before this chunk
+  long run = 0;  // positions before this chunk
   UnitPos p{0, 0, 1, 0};
   for (int base = 0; base < a.num_seqs; base += 64) {
     const int b = base + lane;
-    const int n = b < a.num_seqs ? unit_steps(a.ctx_lens[b], a.max_ctx) : 0;
-    const int c = b < a.num_seqs ? n + kUnitCost : 0;
-    const int incl = wave_incl_scan_i(c);
-    const int first = run + incl - c;  // first position of sequence b
-    const int last = run + incl;       // one past its last
+    const int n = b < a.num_seqs ? unit_steps(a.ctx_lens[b]) : 0;
+    const long c = b < a.num_seqs ? n + kUnitCost : 0;
+    const long incl = wave_incl_scan_l(c);
+    const long first = run + incl - c;  // first position of sequence b
+    const long last = run + incl;       // one past its last
     const unsigned long long hit =
         __builtin_amdgcn_ballot_w64(b < a.num_seqs && first <= s0 && s0 < last);
     if (hit) {
       const int l = __builtin_ffsll((long long)hit) - 1;
       p.b = base + l;
       p.n = __builtin_amdgcn_readfirstlane(__shfl(n, l));
-      p.g = __builtin_amdgcn_readfirstlane(__shfl(first, l));
+      p.g = uniform_l(__shfl(first, l));
       return p;
     }
-    run += __builtin_amdgcn_readfirstlane(__shfl(incl, 63));
+    run += uniform_l(__shfl(incl, 63));
   }
   return p;
 }
@@ -178,11 +190,11 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
   const int NG = max(1, a.num_waves / H);
   const int grp = wave / H, head = wave - grp * H;
   if (grp >= NG) return;
-  const int total = __builtin_amdgcn_readfirstlane(total_steps_per_head(a));
-  const int per = max(a.min_steps, (total + NG - 1) / NG);
-  const int s0 = grp * per;
+  const long total = uniform_l(total_steps_per_head(a));
+  const long per = max((long)a.min_steps, (total + NG - 1) / NG);
+  const long s0 = grp * per;
   if (s0 >= total) return;
-  const int s1 = min(total, s0 + per);
+  const long s1 = min(total, s0 + per);
   UnitPos u = locate(a, s0);
   u.kvh = head;
 
@@ -198,14 +210,14 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
                     uu.kvh, H, a.bs_log2, a.num_blocks, c};
   };
   auto unit_ctx = [&](const UnitPos& uu) -> int {
-    return min(__builtin_amdgcn_readfirstlane(a.ctx_lens[uu.b]), a.max_ctx);
+    return clamp_ctx(__builtin_amdgcn_readfirstlane(a.ctx_lens[uu.b]));
   };
 
   // ---- the first unit: window and the first kDepth steps of loads
-  int lbeg = max(s0 - (u.g + kUnitCost), 0);  // first local step of the unit in the slice
+  int lbeg = (int)max(s0 - (u.g + kUnitCost), 0L);  // first local step of the unit in the slice
   int ctx = unit_ctx(u);
-  int sb = u.g + kUnitCost;  // global position of the unit's step 0
-  int lend = min(u.n, s1 - sb);  // steps of this unit in the slice: [lbeg, lend)
+  long sb = u.g + kUnitCost;  // global position of the unit's step 0
+  int lend = (int)min((long)u.n, s1 - sb);  // steps of this unit in the slice: [lbeg, lend)
   if (lend <= lbeg) return;  // the slice ends inside the unit's overhead: the next group has it
   PoolView pv = make_pv(u, ctx);
   TableWindow win;
@@ -266,9 +278,9 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
     if (has_next) {
       un.g += u.n + kUnitCost;
       ++un.b;
-      un.n = unit_steps(__builtin_amdgcn_readfirstlane(a.ctx_lens[un.b]), a.max_ctx);
+      un.n = unit_steps(__builtin_amdgcn_readfirstlane(a.ctx_lens[un.b]));
       ctx_n = unit_ctx(un);
-      lend_n = min(un.n, s1 - (un.g + kUnitCost));
+      lend_n = (int)min((long)un.n, s1 - (un.g + kUnitCost));
       if (BIG && ctx_n > 0 && lend_n > 0) win_n.fill(a.tables + (long)un.b * a.table_stride, a.table_stride, 0);
     }
     const PoolView pv_n = make_pv(un, ctx_n);
@@ -313,7 +325,7 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
                 (uint32_t)((slot * a.rows + r) * 8), 0, kCoherent);
         }
       }
-      const int wa = sb / per, wb = (sb + u.n - 1) / per;  // groups holding the pieces
+      const int wa = (int)(sb / per), wb = (int)((sb + u.n - 1) / per);  // groups holding the pieces
       const int unit = u.b * H + u.kvh;
       // the piece's stores are complete (hence visible device-wide) before
       // the counter moves
@@ -332,7 +344,7 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
         if (lane == 0) __hip_atomic_store(a.counters + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         // group wa saw this unit first iff its slice began inside the unit's
         // range; the piece of group p sits in the slots of wave p H + head
-        const long slot_a = 2L * (wa * H + head) + (wa * per >= u.g ? 0 : 1);
+        const long slot_a = 2L * (wa * H + head) + ((long)wa * per >= u.g ? 0 : 1);
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
           const int r = nt * 16 + n;
@@ -485,9 +497,23 @@ DecodeFn pick_d(int d, int nt) {
   return nullptr;
 }
 
-// Kernel table of one compute type; each is instantiated in its own
-// translation unit (hpa_decode_{f32,f16,bf16}.hip) so the builds run in
-// parallel.
+// Kernel tables, one per (compute type, KV storage, scale type); each is
+// instantiated in its own translation unit (hpa_decode_<q>_<kv>.hip) so the
+// builds run in parallel.
+#define HPA_DECODE_TABLES(X) \
+  X(F32, F32, F32)           \
+  X(F32, I8, F16)            \
+  X(F32, I8, F32)            \
+  X(F16, F16, F32)           \
+  X(F16, I8, F16)            \
+  X(F16, I8, F32)            \
+  X(BF16, BF16, F32)         \
+  X(BF16, I8, F16)           \
+  X(BF16, I8, F32)
+#define HPA_EXTERN_TABLE(CT, KVT, ST) extern template DecodeFn pick_d<CT, KVT, ST>(int, int);
+HPA_DECODE_TABLES(HPA_EXTERN_TABLE)
+#undef HPA_EXTERN_TABLE
+
 template <class CT>
 DecodeFn pick_kv(int kv_dtype, int scale_dtype, int d, int nt) {
   if (kv_dtype == HPA_I8) {
@@ -498,9 +524,5 @@ DecodeFn pick_kv(int kv_dtype, int scale_dtype, int d, int nt) {
   if (kv_dtype != CT::code) return nullptr;
   return pick_d<CT, CT, F32>(d, nt);
 }
-
-extern template DecodeFn pick_kv<F32>(int, int, int, int);
-extern template DecodeFn pick_kv<F16>(int, int, int, int);
-extern template DecodeFn pick_kv<BF16>(int, int, int, int);
 
 }  // namespace hpa

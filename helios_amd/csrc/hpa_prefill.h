@@ -19,20 +19,47 @@ struct PrefillArgs {
   const int32_t* cu_q;
   const int32_t* q_pos;
   const int32_t* ctx_lens;
-  int num_seqs, num_q_heads, num_kv_heads, group;
+  int num_seqs;
+  // rows of q / out: tokens at or past it are never read or written, so
+  // metadata that disagrees with the tensors cannot address memory outside them
+  int num_tokens;
+  int num_q_heads, num_kv_heads, group;
   int bs_log2, num_blocks;
   float scale_log2;
   // > 0: a speculative verify, uniform_q query tokens per sequence.  cu_q and
   // q_pos are not read: sequence b's tokens are [b uniform_q, (b + 1)
   // uniform_q) and its first token sits at ctx_lens[b] - uniform_q.
-  // Honoured by the MFMA kernel only.
   int uniform_q;
 };
+
+// Sequence b's query tokens [q0, q0 + qn), the first at position pos0, with
+// qn cut at num_tokens.
+struct SeqSpan {
+  int q0, qn, pos0;
+};
+__device__ __forceinline__ SeqSpan seq_span(const PrefillArgs& a, int b) {
+  SeqSpan sp;
+  if (a.uniform_q > 0) {
+    sp = {b * a.uniform_q, a.uniform_q, a.ctx_lens[b] - a.uniform_q};
+  } else {
+    const int q0 = a.cu_q[b];
+    sp = {q0, a.cu_q[b + 1] - q0, a.q_pos[b]};
+  }
+  sp.qn = max(0, min(sp.qn, a.num_tokens - sp.q0));
+  if (sp.q0 < 0) sp.qn = 0;
+  return sp;
+}
 
 // LDS-tiled 32x32 MFMA prefill for fp16 / bf16 queries over pools of the
 // same dtype or int8 pools (fp16 / fp32 scales), head_dim 64 or 128 and
 // block_size >= 16; returns false (launching nothing) for other shapes.
 bool launch_prefill_mfma(const PrefillArgs& a, int q_dtype, int kv_dtype, int scale_dtype, int head_dim,
                          int max_q_len, hipStream_t s);
+
+// The generic prefill kernel (any supported dtype, head_dim and block size);
+// returns HPA_OK or an HPA_ERR_* status (with its message) for shapes it
+// has no kernel for.
+int launch_prefill_generic(const PrefillArgs& a, int q_dtype, int kv_dtype, int scale_dtype, int head_dim,
+                           int max_q_len, hipStream_t s);
 
 }  // namespace hpa

@@ -8,6 +8,10 @@
 // causal mask `k_pos > start_pos + i` (paged_attn.py:401-404) restricted to
 // the gathered context (paged_attn.py:391).
 //
+// A verify launch (uniform_q > 0, from hpa_paged_decode) gives every sequence
+// uniform_q tokens ending at context_len[b] - 1 and reads neither cu_q nor
+// q_pos.  Tokens at or past num_tokens are never read or written.
+//
 // Work decomposition: the (token, head-in-group) rows of each (sequence, KV
 // head) are cut into tiles of NW * NT * 16 rows, one workgroup per tile; each
 // wave owns NT * 16 consecutive rows and streams keys [0, its last row's
@@ -18,8 +22,6 @@
 #include "hpa_prefill.h"
 
 namespace hpa {
-
-
 
 constexpr int kPrefillWaves = 4;
 constexpr int kPrefillNT = 2;
@@ -32,13 +34,13 @@ __global__ __launch_bounds__(64 * NW) void prefill_kernel(const PrefillArgs a) {
   const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int G = a.group;
-  const int q0 = a.cu_q[b];
-  const int T = a.cu_q[b + 1] - q0;
-  const int rows = T * G;
+  const SeqSpan sp = seq_span(a, b);
+  const int q0 = sp.q0;
+  const int rows = sp.qn * G;
   const int row_base = (blockIdx.x * NW + w) * NT * 16;
   if (row_base >= rows) return;  // this kernel has no barriers
   const int ctx = a.ctx_lens[b];
-  const int pos0 = a.q_pos[b];
+  const int pos0 = sp.pos0;
   const q_t* q = reinterpret_cast<const q_t*>(a.q);
   q_t* out = reinterpret_cast<q_t*>(a.out);
   auto row_off = [&](int r) -> long {
@@ -142,6 +144,23 @@ static PrefillFn pick_prefill(int q_dtype, int kv_dtype, int scale_dtype, int d)
   return nullptr;
 }
 
+int launch_prefill_generic(const PrefillArgs& a, int q_dtype, int kv_dtype, int scale_dtype, int head_dim,
+                           int max_q_len, hipStream_t s) {
+  PrefillFn fn = pick_prefill(q_dtype, kv_dtype, scale_dtype, head_dim);
+  if (!fn)
+    return fail(HPA_ERR_UNSUPPORTED,
+                "paged prefill: no kernel for q dtype %d, kv dtype %d, scale dtype %d, head_dim %d", q_dtype,
+                kv_dtype, scale_dtype, head_dim);
+  const long rows = (long)max_q_len * a.group;
+  const long per_wg = (long)kPrefillWaves * kPrefillNT * 16;
+  const long gx = (rows + per_wg - 1) / per_wg;
+  if (gx > 0x7fffffffL || a.num_seqs > 65535 || a.num_kv_heads > 65535)
+    return fail(HPA_ERR_UNSUPPORTED, "paged prefill: %d sequences x %ld rows is too large a grid", a.num_seqs,
+                rows);
+  fn(a, dim3((unsigned)gx, (unsigned)a.num_kv_heads, (unsigned)a.num_seqs), s);
+  return HPA_OK;
+}
+
 }  // namespace hpa
 
 using namespace hpa;
@@ -152,24 +171,23 @@ extern "C" int hpa_paged_prefill(const void* q, void* out, int q_dtype, const vo
                                  const int32_t* block_tables, int table_stride,
                                  const int32_t* cu_q_lens, const int32_t* q_positions,
                                  const int32_t* context_lens, int num_seqs, int max_q_len,
-                                 int num_q_heads, int num_kv_heads, int head_dim, int block_size,
-                                 int num_blocks, float sm_scale, hipStream_t stream) {
-  if (num_seqs == 0 || max_q_len == 0) return HPA_OK;
+                                 int num_tokens, int num_q_heads, int num_kv_heads, int head_dim,
+                                 int block_size, int num_blocks, float sm_scale, hipStream_t stream) {
+  if (num_seqs == 0 || max_q_len == 0 || num_tokens == 0) return HPA_OK;
   if (!q || !out || !k_pool || !v_pool || !block_tables || !cu_q_lens || !q_positions ||
       !context_lens)
     return fail(HPA_ERR_ARG, "hpa_paged_prefill: null pointer argument");
-  if (num_seqs < 0 || max_q_len < 0 || num_q_heads <= 0 || num_kv_heads <= 0 ||
+  if (num_seqs < 0 || max_q_len < 0 || num_tokens < 0 || num_q_heads <= 0 || num_kv_heads <= 0 ||
       num_q_heads % num_kv_heads || num_blocks <= 0 || table_stride <= 0)
-    return fail(HPA_ERR_ARG, "hpa_paged_prefill: bad shape (seqs %d, max_q %d, Hq %d, Hkv %d)",
-                num_seqs, max_q_len, num_q_heads, num_kv_heads);
+    return fail(HPA_ERR_ARG, "hpa_paged_prefill: bad shape (seqs %d, max_q %d, tokens %d, Hq %d, Hkv %d)",
+                num_seqs, max_q_len, num_tokens, num_q_heads, num_kv_heads);
   const int bsl = ilog2_exact(block_size);
   if (bsl < 2 || bsl > 10)
     return fail(HPA_ERR_UNSUPPORTED,
                 "hpa_paged_prefill: block_size %d must be a power of two in [4, 1024]", block_size);
   if (kv_dtype == HPA_I8 && (!k_scale || !v_scale))
     return fail(HPA_ERR_ARG, "hpa_paged_prefill: int8 KV needs k_scale and v_scale");
-  PrefillFn fn = pick_prefill(q_dtype, kv_dtype, scale_dtype, head_dim);
-  if (!fn)
+  if (!pick_prefill(q_dtype, kv_dtype, scale_dtype, head_dim))
     return fail(HPA_ERR_UNSUPPORTED,
                 "hpa_paged_prefill: no kernel for q dtype %d, kv dtype %d, scale dtype %d, head_dim %d",
                 q_dtype, kv_dtype, scale_dtype, head_dim);
@@ -186,6 +204,7 @@ extern "C" int hpa_paged_prefill(const void* q, void* out, int q_dtype, const vo
   a.q_pos = q_positions;
   a.ctx_lens = context_lens;
   a.num_seqs = num_seqs;
+  a.num_tokens = num_tokens;
   a.num_q_heads = num_q_heads;
   a.num_kv_heads = num_kv_heads;
   a.group = num_q_heads / num_kv_heads;
@@ -195,9 +214,7 @@ extern "C" int hpa_paged_prefill(const void* q, void* out, int q_dtype, const vo
   a.uniform_q = 0;
   if (launch_prefill_mfma(a, q_dtype, kv_dtype, scale_dtype, head_dim, max_q_len, stream))
     return check_launch("hpa_paged_prefill");
-  const long rows = (long)max_q_len * a.group;
-  const long per_wg = (long)kPrefillWaves * kPrefillNT * 16;
-  dim3 grid((unsigned)((rows + per_wg - 1) / per_wg), (unsigned)num_kv_heads, (unsigned)num_seqs);
-  fn(a, grid, stream);
+  const int st = launch_prefill_generic(a, q_dtype, kv_dtype, scale_dtype, head_dim, max_q_len, stream);
+  if (st != HPA_OK) return st;
   return check_launch("hpa_paged_prefill");
 }

@@ -143,16 +143,6 @@ constexpr int kPfLptMax = 512;           // items per XCD up to which workgroups
 // 8j + x, so each XCD schedules its own items longest-first (list
 // scheduling's LPT rule) and a unit's tiles stay on one XCD's L2 whenever the
 // unit count is a multiple of 8.  Returns steps + 1, or 0 for an empty tile.
-// sequence b's query tokens [q0, q0 + qn), the first at position pos0
-struct SeqSpan {
-  int q0, qn, pos0;
-};
-__device__ __forceinline__ SeqSpan seq_span(const PrefillArgs& a, int b) {
-  if (a.uniform_q > 0) return {b * a.uniform_q, a.uniform_q, a.ctx_lens[b] - a.uniform_q};
-  const int q0 = a.cu_q[b];
-  return {q0, a.cu_q[b + 1] - q0, a.q_pos[b]};
-}
-
 __device__ __forceinline__ int item_cost(const PrefillArgs& a, int item, int units, int tiles) {
   const int unit = item % units, tile = tiles - 1 - item / units;
   const int b = unit / a.num_kv_heads;

@@ -43,6 +43,33 @@ def _i32(values, device) -> torch.Tensor:
     return torch.tensor(values, dtype=torch.int32, device=device)
 
 
+def _meta(t: torch.Tensor, name: str, device: torch.device, dim: int) -> torch.Tensor:
+    """A metadata tensor handed to a kernel as-is: it must be an int32,
+    contiguous, ``dim``-dimensional tensor on the kernels' device (an int64
+    tensor would be read as pairs of int32 words)."""
+    if t.dtype != torch.int32:
+        raise ValueError(f"{name} must be int32, got {t.dtype}")
+    if t.dim() != dim:
+        raise ValueError(f"{name} must be {dim}-dimensional, got shape {tuple(t.shape)}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if t.device != torch.device(device):
+        raise ValueError(f"{name} is on {t.device}, the kernels run on {device}")
+    return t
+
+
+def _out_for(query: torch.Tensor, out: Optional[torch.Tensor]) -> torch.Tensor:
+    """A row-major output of query's shape and dtype: the kernels write
+    [tokens, heads, head_dim] densely, whatever strides query came with."""
+    if out is None:
+        return torch.empty(query.shape, dtype=query.dtype, device=query.device)
+    if out.shape != query.shape or out.dtype != query.dtype or out.device != query.device:
+        raise ValueError(f"out must be {query.dtype} {tuple(query.shape)} on {query.device}")
+    if not out.is_contiguous():
+        raise ValueError("out must be contiguous")
+    return out
+
+
 def _check_context(block_ids: Sequence[int], context_len: int, block_size: int,
                    num_blocks: int) -> None:
     """helios' gather preconditions (paged_attn.py:100-104) plus pool bounds."""
@@ -231,7 +258,7 @@ def write_kv(
     _require_gpu(k, "k")
     dev = kv_cache.k_cache.device
     if isinstance(block_tables, torch.Tensor):
-        tables = block_tables
+        tables = _meta(block_tables, "block_tables", dev, 2)
         n_seqs = tables.shape[0]
     else:
         n_seqs = len(block_tables)
@@ -239,7 +266,8 @@ def write_kv(
     if cu_query_lens is not None:
         if max_query_len is None:
             raise ValueError("max_query_len is required with cu_query_lens")
-        if cu_query_lens.dtype != torch.int32 or cu_query_lens.numel() != n_seqs + 1:
+        _meta(cu_query_lens, "cu_query_lens", dev, 1)
+        if cu_query_lens.numel() != n_seqs + 1:
             raise ValueError("cu_query_lens must be int32 [n_seqs + 1]")
         cu_t, max_q = cu_query_lens, int(max_query_len)
     else:
@@ -252,7 +280,10 @@ def write_kv(
         for x in qlens:
             cu.append(cu[-1] + x)
         cu_t, max_q = _i32(cu, dev), (max(qlens) if qlens else 0)
-    starts = start_positions if isinstance(start_positions, torch.Tensor) else _i32(list(start_positions), dev)
+    starts = (_meta(start_positions, "start_positions", dev, 1) if isinstance(start_positions, torch.Tensor)
+              else _i32(list(start_positions), dev))
+    if starts.numel() != n_seqs:
+        raise ValueError(f"start_positions has {starts.numel()} entries for {n_seqs} sequences")
     k = k.contiguous()
     v = v.contiguous()
     ks, vs = kv_cache._scales()
@@ -386,9 +417,12 @@ def paged_attention_decode_hip(
     sequence with context c attending keys [0, c - q_per_seq + t]).
     ``block_tables`` / ``context_lens`` may be Python lists (converted like
     triton_attn.py:156-165) or int32 device tensors; with tensors pass
-    ``max_context_len`` to avoid a device sync.  ``out`` and ``workspace``
-    (uint8, at least ``decode_workspace_bytes(...)``) may be passed in to keep
-    the call allocation-free.
+    ``max_context_len`` to avoid a device sync.  ``max_context_len`` only
+    sizes the launch: every context is honoured as given, and with list
+    contexts a bound below the largest one is rejected.  ``out`` (contiguous,
+    query's shape and dtype) and ``workspace`` (uint8, at least
+    ``decode_workspace_bytes(...)``, zero-filled before its first use) may be
+    passed in to keep the call allocation-free.
     """
     _require_gpu(query, "query")
     n_tok, n_q_heads, head_dim = query.shape
@@ -399,30 +433,36 @@ def paged_attention_decode_hip(
         if t is not None and not t.is_contiguous():
             raise ValueError("KV pools and scales must be contiguous")
     if isinstance(block_tables, torch.Tensor):
-        tables = block_tables
+        tables = _meta(block_tables, "block_tables", dev, 2)
     else:
         tables = _padded_tables(block_tables, dev)
     if isinstance(context_lens, torch.Tensor):
-        lens = context_lens
+        lens = _meta(context_lens, "context_lens", dev, 1)
         if max_context_len is None:
             max_context_len = int(lens.max().item()) if lens.numel() else 0
     else:
+        longest = max((int(c) for c in context_lens), default=0)
         if max_context_len is None:
-            max_context_len = max(context_lens, default=0)
+            max_context_len = longest
+        elif max_context_len < longest:
+            raise ValueError(f"max_context_len {max_context_len} is below a context of {longest}")
         lens = _i32(list(context_lens), dev)
     n_seqs = lens.shape[0]
     if n_tok != n_seqs * q_per_seq:
         raise ValueError(f"query has {n_tok} rows, expected {n_seqs} x {q_per_seq}")
-    if out is None:
-        out = torch.empty_like(query)
+    if tables.shape[0] < n_seqs:
+        raise ValueError(f"block_tables has {tables.shape[0]} rows for {n_seqs} sequences")
+    query = query.contiguous()
+    out = _out_for(query, out)
     if n_seqs == 0:
         return out
-    query = query.contiguous()
     L = lib()
     ws_bytes = L.hpa_decode_workspace_size(
         n_seqs, q_per_seq, n_q_heads, n_kv_heads, head_dim, max_context_len, part_tokens
     )
     if workspace is not None:
+        if workspace.device != dev or not workspace.is_contiguous():
+            raise ValueError(f"workspace must be a contiguous tensor on {dev}")
         if workspace.numel() * workspace.element_size() < ws_bytes:
             raise ValueError(f"workspace holds {workspace.nbytes} bytes, {ws_bytes} needed")
         ws = workspace
@@ -466,6 +506,24 @@ def decode_workspace_bytes(n_seqs: int, q_per_seq: int, n_q_heads: int, n_kv_hea
     """Split-K workspace hpa_paged_decode needs for these shapes."""
     return int(_lib.load_library().hpa_decode_workspace_size(
         n_seqs, q_per_seq, n_q_heads, n_kv_heads, head_dim, max_context_len, part_tokens))
+
+
+def decode_workspace(n_seqs: int, q_per_seq: int, n_q_heads: int, n_kv_heads: int, head_dim: int,
+                     max_context_len: int, device, part_tokens: int = 0) -> torch.Tensor:
+    """A zero-filled, caller-owned decode workspace for these shapes (and
+    any smaller ones).  Pass it as ``workspace=`` to keep calls free of
+    allocation, e.g. under HIP graph capture.  Calls that may overlap need
+    workspaces of their own.  If a call did not complete (a launch error),
+    zero it again (``reset_decode_workspace``) before reusing it."""
+    n = decode_workspace_bytes(n_seqs, q_per_seq, n_q_heads, n_kv_heads, head_dim, max_context_len,
+                               part_tokens)
+    return torch.zeros(max(n, 1), dtype=torch.uint8, device=device)
+
+
+def reset_decode_workspace(workspace: torch.Tensor) -> None:
+    """Return a workspace's split-K arrival counters to zero.  Every call
+    that completes leaves them at zero; this is for a call that did not."""
+    workspace.zero_()
 
 
 def _cache_tensors(kv_cache: PagedKVCache):
@@ -556,6 +614,7 @@ def paged_attention_varlen(
     scale: Optional[float] = None,
     max_query_len: Optional[int] = None,
     cu_query_lens: Optional[torch.Tensor] = None,
+    out: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Causal attention for a ragged batch of prompt chunks in one launch.
 
@@ -565,24 +624,28 @@ def paged_attention_varlen(
     per sequence, which is what reference exec/model.py:303-317 does.
     ``cu_query_lens`` (int32 device tensor [n + 1], the prefix sums of
     ``query_lens``) and ``max_query_len`` may be passed to skip building them
-    per call."""
+    per call.  Device metadata is not read back: query tokens it places at or
+    past ``query``'s last row are neither read nor written, and a sum of
+    ``query_lens`` known on the host must equal the row count."""
     _require_gpu(query, "query")
     n_tok, n_q_heads, head_dim = query.shape
     scale = scale or 1.0 / math.sqrt(head_dim)
     _check_query_dtype(query, kv_cache)
     dev = query.device
     if isinstance(block_tables, torch.Tensor):
-        tables = block_tables
+        tables = _meta(block_tables, "block_tables", dev, 2)
     else:
         for blocks, ctx in zip(block_tables, (context_lens.tolist() if isinstance(context_lens, torch.Tensor) else context_lens)):
             _check_context(blocks, int(ctx), kv_cache.block_size, kv_cache.num_blocks)
         tables = _padded_tables(block_tables, dev)
     if cu_query_lens is not None:
-        cu = cu_query_lens
+        cu = _meta(cu_query_lens, "cu_query_lens", dev, 1)
         n_seqs = cu.numel() - 1
         if max_query_len is None:
             max_query_len = int((cu[1:] - cu[:-1]).max().item()) if n_seqs > 0 else 0
     elif isinstance(query_lens, torch.Tensor):
+        if query_lens.device.type == "cpu" and int(query_lens.sum()) != n_tok:
+            raise ValueError(f"query has {n_tok} rows but query_lens sum to {int(query_lens.sum())}")
         qlens_t = query_lens.to(device=dev, dtype=torch.int32)
         cu = torch.zeros(qlens_t.numel() + 1, dtype=torch.int32, device=dev)
         cu[1:] = torch.cumsum(qlens_t, 0)
@@ -600,17 +663,21 @@ def paged_attention_varlen(
         if max_query_len is None:
             max_query_len = max(ql, default=0)
         n_seqs = len(ql)
-    pos = start_positions if isinstance(start_positions, torch.Tensor) else _i32(list(start_positions), dev)
-    lens = context_lens if isinstance(context_lens, torch.Tensor) else _i32(list(context_lens), dev)
-    out = torch.empty_like(query)
+    pos = (_meta(start_positions, "start_positions", dev, 1) if isinstance(start_positions, torch.Tensor)
+           else _i32(list(start_positions), dev))
+    lens = (_meta(context_lens, "context_lens", dev, 1) if isinstance(context_lens, torch.Tensor)
+            else _i32(list(context_lens), dev))
+    if pos.numel() != n_seqs or lens.numel() != n_seqs or tables.shape[0] < n_seqs:
+        raise ValueError(f"start_positions, context_lens and block_tables must cover {n_seqs} sequences")
+    query = query.contiguous()
+    out = _out_for(query, out)
     if n_seqs == 0 or n_tok == 0:
         return out
-    query = query.contiguous()
     k, v, ks, vs = _cache_tensors(kv_cache)
     st = lib().hpa_paged_prefill(
         ptr(query), ptr(out), DTYPE_CODE[query.dtype], ptr(k), ptr(v), DTYPE_CODE[k.dtype],
         ptr(ks), ptr(vs), DTYPE_CODE[ks.dtype] if ks is not None else 0, ptr(tables),
-        tables.shape[1], ptr(cu), ptr(pos), ptr(lens), n_seqs, max_query_len, n_q_heads,
+        tables.shape[1], ptr(cu), ptr(pos), ptr(lens), n_seqs, max_query_len, n_tok, n_q_heads,
         kv_cache.n_kv_heads, head_dim, kv_cache.block_size, kv_cache.num_blocks, float(scale),
         stream_ptr(dev),
     )

@@ -463,18 +463,22 @@ def write_kv_batched(kv_cache: PagedKVCache, meta: DeviceAttnMeta, k: torch.Tens
 
 
 def batched_attention(query: torch.Tensor, kv_cache: PagedKVCache, meta: DeviceAttnMeta,
-                      scale: Optional[float] = None) -> torch.Tensor:
+                      scale: Optional[float] = None, out: Optional[torch.Tensor] = None,
+                      workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
     """``BatchedAttention.run`` (exec/model.py:287-318) on device metadata:
     a decode batch goes to the decode kernel (q_per_seq query tokens per
     sequence, the speculative verify form when above 1), anything else to the
-    ragged causal prefill, each one launch."""
+    ragged causal prefill, each one launch.  ``out`` and a caller-owned
+    decode ``workspace`` (``decode_workspace``) make the call allocate
+    nothing, as code under HIP graph capture needs."""
     if query.shape[0] != meta.n_tokens:
         raise ValueError(f"query has {query.shape[0]} rows, the batch has {meta.n_tokens} tokens")
     if meta.is_decode:
         ks, vs = kv_cache._scales()
         return paged_attention_decode_hip(
             query, kv_cache.k_cache, kv_cache.v_cache, meta.block_tables, meta.context_lens, scale,
-            ks, vs, q_per_seq=max(meta.max_query_len, 1), max_context_len=meta.max_context_len)
+            ks, vs, q_per_seq=max(meta.max_query_len, 1), max_context_len=meta.max_context_len,
+            out=out, workspace=workspace)
     return paged_attention_varlen(
         query, kv_cache, meta.block_tables, None, meta.start_positions, meta.context_lens, scale,
-        max_query_len=meta.max_query_len, cu_query_lens=meta.cu_query_lens)
+        max_query_len=meta.max_query_len, cu_query_lens=meta.cu_query_lens, out=out)

@@ -59,7 +59,8 @@ int hpa_version(void);
 const char* hpa_last_error(void);
 
 /* Bytes of split-K workspace hpa_paged_decode needs for these shapes
- * (0 when no sequence is split).  part_tokens: 0 = library default. */
+ * (0 when no sequence is split, or when the shapes run on the prefill
+ * kernels).  part_tokens: 0 = library default. */
 size_t hpa_decode_workspace_size(int num_seqs, int q_per_seq, int num_q_heads, int num_kv_heads,
                                  int head_dim, int max_context_len, int part_tokens);
 
@@ -72,22 +73,28 @@ size_t hpa_decode_workspace_size(int num_seqs, int q_per_seq, int num_q_heads, i
  *                 (F32, F16 or BF16; out has the same dtype)
  *   k/v_pool      kv_dtype == q_dtype, or HPA_I8 with k/v_scale of
  *                 scale_dtype (F16 as helios stores them, or F32)
- *   context_lens  int32 [num_seqs]; every value <= max_context_len
+ *   context_lens  int32 [num_seqs], each at most 2^30
+ *   max_context_len  an upper bound of context_lens, used only to size the
+ *                 launch and the workspace: every context is honoured as
+ *                 given (one above the bound makes the call slower, never
+ *                 wrong)
  * Token t of sequence b attends keys [0, context_lens[b] - q_per_seq + t]
  * (helios' causal rule, paged_attn.py:401-404, with start_pos = context -
  * q_per_seq).  An empty context yields zeros.  Softmax scale sm_scale.
- * The query rows of one KV head ((num_q_heads / num_kv_heads) * q_per_seq)
- * must not exceed 64; use hpa_paged_prefill beyond that.  33 to 64 rows run
- * on the MFMA prefill kernel when it takes the shape (fp16 / bf16 queries,
- * head_dim 64 or 128, block_size >= 16), with the same results as
- * hpa_paged_prefill over the same tokens; the workspace is then unused.
+ * Any number of query rows per KV head ((num_q_heads / num_kv_heads) *
+ * q_per_seq) is taken: above 32 they run on the prefill kernels (the MFMA
+ * one when it takes the shape: fp16 / bf16 queries, head_dim 64 or 128,
+ * block_size >= 16), with the same results as hpa_paged_prefill over the
+ * same tokens; the workspace is then unused.
  * part_tokens: smallest share of the context, in tokens, one wave streams
  * (0 = library default); it changes only the summation order.
  * workspace: at least hpa_decode_workspace_size(...) bytes of device memory
  * (may be NULL if that is 0), zero-filled before its first use.  It holds
  * per-(sequence, KV head) arrival counters that every completed call leaves
  * at zero again, so one workspace serves any number of calls ordered on one
- * stream; calls that may run concurrently need separate workspaces. */
+ * stream; calls that may run concurrently need separate workspaces.  A call
+ * that did not complete (a launch error, a device reset) may leave counters
+ * set: zero-fill the workspace again before reusing it. */
 int hpa_paged_decode(const void* q, void* out, int q_dtype, const void* k_pool, const void* v_pool,
                      int kv_dtype, const void* k_scale, const void* v_scale, int scale_dtype,
                      const int32_t* block_tables, int table_stride, const int32_t* context_lens,
@@ -104,14 +111,17 @@ int hpa_paged_decode(const void* q, void* out, int q_dtype, const void* k_pool, 
  *   q_positions   int32 [num_seqs]: absolute position of each sequence's first
  *                 query token (helios' start_pos)
  *   context_lens  int32 [num_seqs]: keys [0, context) exist
+ *   num_tokens    rows of q and out: query tokens at or past it are neither
+ *                 read nor written, whatever cu_q_lens says
  * Query token i of sequence b attends keys [0, min(q_positions[b] + i + 1,
  * context_lens[b])).  Rows with no key yield zeros. */
 int hpa_paged_prefill(const void* q, void* out, int q_dtype, const void* k_pool, const void* v_pool,
                       int kv_dtype, const void* k_scale, const void* v_scale, int scale_dtype,
                       const int32_t* block_tables, int table_stride, const int32_t* cu_q_lens,
                       const int32_t* q_positions, const int32_t* context_lens, int num_seqs,
-                      int max_q_len, int num_q_heads, int num_kv_heads, int head_dim,
-                      int block_size, int num_blocks, float sm_scale, hipStream_t stream);
+                      int max_q_len, int num_tokens, int num_q_heads, int num_kv_heads,
+                      int head_dim, int block_size, int num_blocks, float sm_scale,
+                      hipStream_t stream);
 
 /* Scatter new K/V into the pool; int8 pools quantise on the fly.
  * Replaces PagedKVCache.write (paged_attn.py:57-85) and

@@ -26,6 +26,11 @@ each one is pinned (tests/test_oracle.py):
                            tests/parity/test_parity.py:77-86, chunked ==
                            single-shot, GQA head mapping, order invariance
   paged_verify_batched     equals per-sequence prefill (runner.py:354-362)
+  paged_varlen             per-token brute force on each sequence's dense
+                           K/V across a ragged batch (row offsets, an empty
+                           chunk, per-sequence starts, a context cutting a
+                           chunk's causal reach), with planted offset /
+                           start / table mistakes shown to fail
 
 No function here is "parity unpinned".  The math runs in float64 unless a
 function says otherwise; empty softmax rows give NaN exactly as helios'

@@ -97,9 +97,12 @@ def test_argument_errors_return_status_without_a_gpu(lib):
     st = lib.hpa_paged_decode(dummy, dummy, 1, dummy, dummy, 1, None, None, 0, dummy, 1, dummy,
                               1, 1, 4, 2, 48, 16, 8, 16, 1.0, 0, None, 0, None)
     assert st == _lib.HPA_ERR_UNSUPPORTED and b"head_dim 48" in lib.hpa_last_error()
+    # more than 64 rows per KV head go to the prefill kernels, which refuse
+    # head_dim 48 before launching anything
     st = lib.hpa_paged_decode(dummy, dummy, 1, dummy, dummy, 1, None, None, 0, dummy, 1, dummy,
-                              1, 9, 8, 1, 64, 16, 8, 16, 1.0, 0, None, 0, None)
-    assert st == _lib.HPA_ERR_UNSUPPORTED and b"exceed 64" in lib.hpa_last_error()
+                              1, 9, 8, 1, 48, 16, 8, 16, 1.0, 0, None, 0, None)
+    assert st == _lib.HPA_ERR_UNSUPPORTED and b"head_dim 48" in lib.hpa_last_error()
+    assert lib.hpa_decode_workspace_size(4, 9, 8, 1, 64, 4096, 0) == 0
     # int8 without scales
     st = lib.hpa_kv_write(dummy, dummy, 1, dummy, dummy, 3, None, None, 1, dummy, 1, dummy, dummy,
                           1, 1, 2, 64, 16, 8, None)
@@ -119,4 +122,7 @@ def test_argument_errors_return_status_without_a_gpu(lib):
     assert lib.hpa_step_tables(None, 0, None, 0, None, 0, 0, None, 0, None) == _lib.HPA_OK
     # empty batches are no-ops
     assert lib.hpa_paged_prefill(None, None, 0, None, None, 0, None, None, 0, None, 1, None, None,
-                                 None, 0, 0, 1, 1, 64, 16, 1, 1.0, None) == _lib.HPA_OK
+                                 None, 0, 0, 0, 1, 1, 64, 16, 1, 1.0, None) == _lib.HPA_OK
+    st = lib.hpa_paged_prefill(dummy, dummy, 1, dummy, dummy, 1, None, None, 0, dummy, 1, dummy, dummy,
+                               dummy, 2, 4, -1, 8, 2, 64, 16, 8, 1.0, None)
+    assert st == _lib.HPA_ERR_ARG and b"tokens -1" in lib.hpa_last_error()

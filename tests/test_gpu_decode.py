@@ -284,3 +284,97 @@ def test_stream_k_many_pieces_and_empty_units(quant):
     other = paged_attention_decode_hip(q, cache.k_cache, cache.v_cache, tables, lens,
                                        k_scale=ks, v_scale=vs)
     assert max_abs(to_np(got), to_np(other)) <= 2e-3
+
+
+@pytest.mark.parametrize("quant", [False, True])
+@pytest.mark.parametrize("Hq,Hkv,T,D,dtype", [(14, 2, 13, 64, torch.float16), (32, 8, 20, 128, torch.float16),
+                                              (8, 1, 17, 128, torch.bfloat16)])
+def test_verify_beyond_64_rows_per_kv_head(Hq, Hkv, T, D, dtype, quant):
+    """Any gamma verifies, as helios' runner does (exec/runner.py:330-362):
+    Qwen's G = 7 with gamma = 12 (91 rows per KV head), G = 4 with 20 tokens
+    (80 rows) and G = 8 with 17 (136 rows, more than one 128-row tile) run on
+    the MFMA prefill kernel and equal paged_attention_varlen over the same
+    tokens bit for bit, and the oracle."""
+    print(f"verify > 64 rows: {Hq}/{Hkv} x {T}, D {D}, {dtype}, int8 {quant}", flush=True)
+    lens = [T, T + 3, 64, 300, 1100]
+    cache, tables, q = _case(110 + Hq + T, len(lens), lens, Hq, Hkv, D, 16, dtype, quant=quant, q_per_seq=T)
+    got = paged_attention_verify_batched(q, cache, tables, lens, T)
+    same = paged_attention_varlen(q, cache, tables, [T] * len(lens), [c - T for c in lens], lens)
+    assert torch.equal(got, same)
+    pool = pool_dequantized(cache) if quant else pool_of(cache)
+    want = R.paged_verify_batched(to_np(q).astype(np.float32), pool, tables, lens, T)
+    _check(got, want, dtype, "verify > 64 rows")
+
+
+@pytest.mark.parametrize("D,bs,dtype", [(32, 16, torch.float16), (128, 8, torch.float16), (64, 16, torch.float32)])
+def test_verify_beyond_64_rows_on_the_generic_prefill_kernel(D, bs, dtype):
+    """More than 64 rows on shapes the MFMA kernel does not take (head_dim 32,
+    block size 8, fp32) run on the generic prefill kernel's verify mode."""
+    print(f"verify > 64 rows, generic kernel: D {D}, block {bs}, {dtype}", flush=True)
+    T, lens = 9, [9, 20, 77, 300]
+    cache, tables, q = _case(120 + D + bs, len(lens), lens, 16, 2, D, bs, dtype, q_per_seq=T)
+    got = paged_attention_verify_batched(q, cache, tables, lens, T)
+    _check(got, _oracle_decode(cache, q, tables, lens, q_per_seq=T), dtype, f"generic verify D={D}")
+    same = paged_attention_varlen(q, cache, tables, [T] * len(lens), [c - T for c in lens], lens)
+    assert torch.equal(got, same)
+
+
+def test_permuted_query_layouts_give_row_major_results():
+    """A dense but permuted query ([T, Hq, D] made by transposing [Hq, T, D])
+    is attended as its values say, and the result is a row-major tensor, for
+    decode, verify and the ragged prefill alike."""
+    lens = [40, 77, 300]
+    cache, tables, q = _case(130, len(lens), lens, 8, 2, 64, 16, torch.float16, q_per_seq=3)
+    qp = q.permute(1, 0, 2).contiguous().permute(1, 0, 2)  # same values, strides (D, rows*D, 1)
+    assert not qp.is_contiguous() and torch.equal(qp, q)
+    v1 = paged_attention_verify_batched(qp, cache, tables, lens, 3)
+    assert v1.is_contiguous() and torch.equal(v1, paged_attention_verify_batched(q, cache, tables, lens, 3))
+    q1 = q[::3]
+    q1p = q1.permute(1, 0, 2).contiguous().permute(1, 0, 2)
+    d1 = paged_attention_decode_batched(q1p, cache, tables, lens)
+    assert d1.is_contiguous() and torch.equal(d1, paged_attention_decode_batched(q1.contiguous(), cache, tables, lens))
+    p1 = paged_attention_varlen(qp, cache, tables, [3] * 3, [c - 3 for c in lens], lens)
+    p0 = paged_attention_varlen(q, cache, tables, [3] * 3, [c - 3 for c in lens], lens)
+    assert p1.is_contiguous() and torch.equal(p1, p0)
+    _check(p1, _oracle_decode(cache, q, tables, lens, q_per_seq=3), torch.float16, "permuted varlen")
+
+
+def test_context_above_the_launch_bound_is_honoured():
+    """max_context_len only sizes the launch: a device-tensor context above
+    it is attended in full (the result equals the call with the right bound),
+    and list contexts reject a bound below their largest one."""
+    lens = [50, 700, 3]
+    cache, tables, q = _case(140, 3, lens, 8, 2, 64, 16, torch.float16)
+    width = max(len(t) for t in tables)
+    tt = torch.tensor([t + [0] * (width - len(t)) for t in tables], dtype=torch.int32, device="cuda")
+    lt = torch.tensor(lens, dtype=torch.int32, device="cuda")
+    right = paged_attention_decode_hip(q, cache.k_cache, cache.v_cache, tt, lt, max_context_len=700)
+    stale = paged_attention_decode_hip(q, cache.k_cache, cache.v_cache, tt, lt, max_context_len=64)
+    _check(stale, _oracle_decode(cache, q, tables, lens), torch.float16, "stale bound")
+    assert max_abs(to_np(right), to_np(stale)) <= 2e-3
+    with pytest.raises(ValueError, match="below a context"):
+        paged_attention_decode_hip(q, cache.k_cache, cache.v_cache, tables, lens, max_context_len=64)
+
+
+def test_metadata_tensors_are_validated():
+    """int64, non-contiguous or misplaced metadata tensors are refused rather
+    than read as int32 words."""
+    lens = [50, 70]
+    cache, tables, q = _case(150, 2, lens, 8, 2, 64, 16, torch.float16)
+    width = max(len(t) for t in tables)
+    tt = torch.tensor([t + [0] * (width - len(t)) for t in tables], dtype=torch.int32, device="cuda")
+    lt = torch.tensor(lens, dtype=torch.int32, device="cuda")
+    k, v = cache.k_cache, cache.v_cache
+    with pytest.raises(ValueError, match="int32"):
+        paged_attention_decode_hip(q, k, v, tt.long(), lt, max_context_len=70)
+    with pytest.raises(ValueError, match="int32"):
+        paged_attention_decode_hip(q, k, v, tt, lt.long(), max_context_len=70)
+    with pytest.raises(ValueError, match="contiguous"):
+        paged_attention_decode_hip(q, k, v, tt.t().contiguous().t(), lt, max_context_len=70)
+    with pytest.raises(ValueError, match="is on cpu"):
+        paged_attention_decode_hip(q, k, v, tt.cpu(), lt, max_context_len=70)
+    with pytest.raises(ValueError, match="out must be contiguous"):
+        paged_attention_decode_hip(q, k, v, tt, lt, max_context_len=70,
+                                   out=torch.empty(8, 2, 64, dtype=torch.float16, device="cuda").transpose(0, 1))
+    with pytest.raises(ValueError, match="sum to"):
+        paged_attention_varlen(q, cache, tt, torch.tensor([1, 2], dtype=torch.int32), lt - 1, lt)

@@ -1,9 +1,10 @@
 """A multi-layer decode / verify step captured in a HIP graph.
 
-With the step's metadata on the device (DeviceBlockTables) every layer's
-write_kv_batched + batched_attention is launches only -- no host work, no
-synchronisation, no allocation once warm -- so the whole step can be captured
-and replayed.  The decode kernel's split-K counters are returned to zero by
+With the step's metadata on the device (DeviceBlockTables) and the outputs
+and a decode workspace owned by the caller, every layer's write_kv_batched +
+batched_attention is launches only -- no host work, no synchronisation, no
+allocation (the capture is checked to allocate nothing) -- so the whole step
+can be captured and replayed.  The decode kernel's split-K counters are returned to zero by
 the kernel itself, so a replay needs no memset node.  Each replay here runs
 after eager work and a synchronisation, with new inputs copied into the
 captured tensors, and must equal the same calls made eagerly on twin caches,
@@ -66,24 +67,34 @@ def test_captured_step_replays_equal_eager(quant, q_per_seq):
         for t in (q, k, v):
             t.copy_(torch.randn(t.shape, generator=gen, device="cuda").half())
 
-    def step(caches):
-        outs = []
+    def owned():
+        return ([torch.empty(n_tok, Hq, D, device="cuda", dtype=torch.float16) for _ in range(layers)],
+                H.decode_workspace(B, q_per_seq, Hq, Hkv, D, meta.max_context_len, "cuda"))
+
+    graph_owned, eager_owned = owned(), owned()
+
+    def step(caches, own):
+        outs, ws = own
         for li, c in enumerate(caches):
             H.write_kv_batched(c, meta, k[li], v[li])
-            outs.append(H.batched_attention(q[li], c, meta, 0.125))
+            H.batched_attention(q[li], c, meta, 0.125, out=outs[li], workspace=ws)
         return outs
 
     fill()
-    step(graph_caches)  # warm: workspace sized, launch configuration cached
-    step(eager_caches)
+    step(graph_caches, graph_owned)  # warm: launch configuration cached
+    step(eager_caches, eager_owned)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        graph_out = step(graph_caches)
+        # counted inside the capture: torch's own capture set-up is not ours
+        allocs = torch.cuda.memory_stats()["allocation.all.allocated"]
+        graph_out = step(graph_caches, graph_owned)
+        allocs = torch.cuda.memory_stats()["allocation.all.allocated"] - allocs
     torch.cuda.synchronize()
+    assert allocs == 0, f"the captured step allocated {allocs} times"
     for rep in range(4):
         fill()
-        want = step(eager_caches)  # eager work between the replays
+        want = step(eager_caches, eager_owned)  # eager work between the replays
         torch.cuda.synchronize()
         g.replay()
         torch.cuda.synchronize()

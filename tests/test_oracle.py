@@ -264,6 +264,84 @@ def test_helios_cpu_routes_agree_with_the_oracle():
                                R.paged_prefill(qp, pool, tables[1], 55, 60), atol=2e-6)
 
 
+def _ragged_case(seed):
+    """Three sequences written through scattered blocks of one pool: token
+    counts (3, 0, 4) -- the middle chunk empty -- at start positions (2, 5, 0)
+    with contexts (5, 5, 3), the last one shorter than its chunk's reach."""
+    rng = RNG(seed)
+    bs, Hkv, Hq, D = 2, 2, 4, 3
+    pool = R.PagedPool(16, bs, Hkv, D)
+    tables = [[7, 2, 11], [4, 0, 9], [13, 5]]
+    ctxs, starts, qlens = [5, 5, 3], [2, 5, 0], [3, 0, 4]
+    dense = []
+    for t, c in zip(tables, ctxs):
+        k = rng.standard_normal((c, Hkv, D)).astype(np.float32)  # the pool's storage dtype
+        v = rng.standard_normal((c, Hkv, D)).astype(np.float32)
+        pool.write(t, 0, k, v)
+        dense.append((k, v))
+    q = rng.standard_normal((sum(qlens), Hq, D))
+    return pool, tables, ctxs, starts, qlens, dense, q
+
+
+def _varlen_brute_force(q, dense, ctxs, starts, qlens, scale):
+    """Row by row in pure Python: token i of sequence b (row offset by the
+    earlier chunks) attends the first min(start + i + 1, ctx) keys of that
+    sequence's own dense K/V."""
+    rows, lo = [], 0
+    for (k, v), c, s, n in zip(dense, ctxs, starts, qlens):
+        for i in range(n):
+            rows.append(R.brute_force_attention(q[lo + i:lo + i + 1], k[:c], v[:c], [s + i], scale)[0])
+        lo += n
+    return np.array(rows)
+
+
+def test_varlen_matches_brute_force_on_a_ragged_batch():
+    """paged_varlen (BatchedAttention.run's prefill branch, reference
+    exec/model.py:303-317) against per-token brute force on the dense K/V:
+    row offsets across sequences, an empty chunk, per-sequence start
+    positions and a context that cuts a chunk's causal reach."""
+    pool, tables, ctxs, starts, qlens, dense, q = _ragged_case(21)
+    got = R.paged_varlen(q, pool, tables, qlens, starts, ctxs, 0.6)
+    assert got.shape == q.shape
+    np.testing.assert_allclose(got, _varlen_brute_force(q, dense, ctxs, starts, qlens, 0.6), atol=1e-12)
+
+
+def test_varlen_default_scale_and_empty_batch():
+    pool, tables, ctxs, starts, qlens, dense, q = _ragged_case(22)
+    got = R.paged_varlen(q, pool, tables, qlens, starts, ctxs)
+    np.testing.assert_allclose(got, _varlen_brute_force(q, dense, ctxs, starts, qlens, 1 / math.sqrt(3)),
+                               atol=1e-12)
+    empty = R.paged_varlen(q[:0], pool, [], [], [], [])
+    assert empty.shape == (0, 4, 3)
+
+
+def _varlen_no_offset(q, pool, tables, qlens, starts, ctxs, scale):
+    """Planted mistake: every sequence reads its queries from row 0."""
+    return np.concatenate([R.paged_prefill(q[:n], pool, t, s, c, scale)
+                           for t, n, s, c in zip(tables, qlens, starts, ctxs)])
+
+
+def _varlen_start_zero(q, pool, tables, qlens, starts, ctxs, scale):
+    """Planted mistake: chunks treated as starting at position 0."""
+    return R.paged_varlen(q, pool, tables, qlens, [0] * len(starts), ctxs, scale)
+
+
+def _varlen_swapped_tables(q, pool, tables, qlens, starts, ctxs, scale):
+    """Planted mistake: sequence b attends through the next sequence's table."""
+    return R.paged_varlen(q, pool, tables[1:] + tables[:1], qlens, starts, ctxs, scale)
+
+
+@pytest.mark.parametrize("bad", [_varlen_no_offset, _varlen_start_zero, _varlen_swapped_tables])
+def test_varlen_brute_force_catches_planted_mistakes(bad):
+    pool, tables, ctxs, starts, qlens, dense, q = _ragged_case(23)
+    want = _varlen_brute_force(q, dense, ctxs, starts, qlens, 0.6)
+    try:
+        got = bad(q, pool, tables, qlens, starts, ctxs, 0.6)
+    except (IndexError, ValueError):
+        return  # a planted mistake that fails loudly is caught too
+    assert got.shape != want.shape or not np.allclose(got, want, atol=1e-6)
+
+
 # ------------------------------------------------- planted mistakes get caught
 
 
