@@ -24,6 +24,9 @@ HPA_ERR_UNSUPPORTED = 2
 HPA_ERR_WORKSPACE = 3
 HPA_ERR_LAUNCH = 4
 
+# bytes of the static per-GPU scratch of hpa_paged_decode_noalloc
+HPA_NOALLOC_SCRATCH_BYTES = 64 << 20
+
 HPA_F32 = 0
 HPA_F16 = 1
 HPA_BF16 = 2
@@ -51,6 +54,12 @@ SIGNATURES = {
         [_c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_int,
          _c_ptr, _c_int, _c_ptr, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
          _c_int, _c_int, _c_float, _c_int, _c_ptr, _c_size, _c_ptr],
+    ),
+    "hpa_paged_decode_noalloc": (
+        _c_int,
+        [_c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr, _c_int,
+         _c_ptr, _c_int, _c_ptr, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+         _c_int, _c_int, _c_float, _c_int, _c_ptr],
     ),
     "hpa_paged_prefill": (
         _c_int,

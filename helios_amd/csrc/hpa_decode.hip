@@ -1,5 +1,7 @@
 // C-ABI of the paged decode / speculative-verify attention (the kernels and
 // their work decomposition are in hpa_decode_impl.h).
+#include <mutex>
+
 #include "hpa_decode_impl.h"
 #include "hpa_prefill.h"
 
@@ -63,14 +65,56 @@ extern "C" size_t hpa_decode_workspace_size(int num_seqs, int q_per_seq, int num
   return ws_bytes(p.waves, rows, head_dim);
 }
 
-extern "C" int hpa_paged_decode(const void* q, void* out, int q_dtype, const void* k_pool,
-                                const void* v_pool, int kv_dtype, const void* k_scale,
-                                const void* v_scale, int scale_dtype, const int32_t* block_tables,
-                                int table_stride, const int32_t* context_lens, int num_seqs,
-                                int q_per_seq, int num_q_heads, int num_kv_heads, int head_dim,
-                                int block_size, int num_blocks, int max_context_len,
-                                float sm_scale, int part_tokens, void* workspace,
-                                size_t workspace_bytes, hipStream_t stream) {
+namespace hpa {
+
+// ---- the workspace of hpa_paged_decode_noalloc: a static array per GPU, for
+// callers that cannot allocate.  In host code `scratch` names a host-side
+// stand-in, not device memory: its device address comes from
+// hipGetSymbolAddress, once per device, and only that address is used.
+constexpr size_t kScratchBytes = (size_t)HPA_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch[kMaxDevices];
+
+// The current device's address of `scratch`, looked up on the first call
+// on that device (with it current) and kept.
+static int scratch_address(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(HPA_ERR_LAUNCH, "hpa_paged_decode_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(HPA_ERR_UNSUPPORTED, "hpa_paged_decode_noalloc: device %d beyond %d", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(HPA_ERR_LAUNCH, "hpa_paged_decode_noalloc: hipGetSymbolAddress(scratch): %s",
+                  hipGetErrorString(e));
+    g_scratch[dev] = p;
+  }
+  *out = g_scratch[dev];
+  return HPA_OK;
+}
+
+// Zeroes the arrival counters [0, n) with vector stores (a kernel, not a
+// memset, so the call stays capturable in a HIP graph).
+__global__ __launch_bounds__(256) void clear_counters_kernel(int* counters, int n) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) counters[i] = 0;
+}
+
+enum class Ws { Caller, Static };
+
+static int paged_decode(const void* q, void* out, int q_dtype, const void* k_pool, const void* v_pool,
+                        int kv_dtype, const void* k_scale, const void* v_scale, int scale_dtype,
+                        const int32_t* block_tables, int table_stride, const int32_t* context_lens,
+                        int num_seqs, int q_per_seq, int num_q_heads, int num_kv_heads, int head_dim,
+                        int block_size, int num_blocks, int max_context_len, float sm_scale,
+                        int part_tokens, void* workspace, size_t workspace_bytes, Ws ws_kind,
+                        hipStream_t stream) {
   if (num_seqs == 0) return HPA_OK;
   if (!q || !out || !k_pool || !v_pool || !block_tables || !context_lens)
     return fail(HPA_ERR_ARG, "hpa_paged_decode: null pointer argument");
@@ -136,6 +180,25 @@ extern "C" int hpa_paged_decode(const void* q, void* out, int q_dtype, const voi
     return fail(HPA_ERR_UNSUPPORTED, "hpa_paged_decode: %d sequences x %d KV heads exceed %ld",
                 num_seqs, num_kv_heads, kMaxUnits);
   const size_t need = ws_bytes(p.waves, rows, head_dim);
+  if (ws_kind == Ws::Static) {
+    if (need > kScratchBytes)
+      return fail(HPA_ERR_WORKSPACE,
+                  "hpa_paged_decode_noalloc: these shapes need %zu bytes of workspace, the static scratch "
+                  "holds %zu; use hpa_paged_decode with a caller-owned workspace",
+                  need, kScratchBytes);
+    if (need) {
+      const int st = scratch_address(&workspace);
+      if (st != HPA_OK) return st;
+      workspace_bytes = kScratchBytes;
+      // the counters this call uses start at zero, whatever an earlier call
+      // that did not complete left there
+      const int units = num_seqs * num_kv_heads;
+      hipLaunchKernelGGL(clear_counters_kernel, dim3((unsigned)((units + 255) / 256)), dim3(256), 0, stream,
+                         reinterpret_cast<int*>(workspace), units);
+      const int cl = check_launch("hpa_paged_decode_noalloc");
+      if (cl != HPA_OK) return cl;
+    }
+  }
   if (need > workspace_bytes || (need && !workspace))
     return fail(HPA_ERR_WORKSPACE, "hpa_paged_decode: workspace of %zu bytes needed, %zu given", need,
                 workspace_bytes);
@@ -168,4 +231,33 @@ extern "C" int hpa_paged_decode(const void* q, void* out, int q_dtype, const voi
   a.ws_o = need ? a.ws_ml + (size_t)p.waves * 2 * rows * 2 : nullptr;
   // workspace offsets follow the cap; the launcher may run fewer waves
   return fn(a, p.waves, stream);
+}
+
+}  // namespace hpa
+
+extern "C" int hpa_paged_decode(const void* q, void* out, int q_dtype, const void* k_pool,
+                                const void* v_pool, int kv_dtype, const void* k_scale,
+                                const void* v_scale, int scale_dtype, const int32_t* block_tables,
+                                int table_stride, const int32_t* context_lens, int num_seqs,
+                                int q_per_seq, int num_q_heads, int num_kv_heads, int head_dim,
+                                int block_size, int num_blocks, int max_context_len,
+                                float sm_scale, int part_tokens, void* workspace,
+                                size_t workspace_bytes, hipStream_t stream) {
+  return paged_decode(q, out, q_dtype, k_pool, v_pool, kv_dtype, k_scale, v_scale, scale_dtype, block_tables,
+                      table_stride, context_lens, num_seqs, q_per_seq, num_q_heads, num_kv_heads, head_dim,
+                      block_size, num_blocks, max_context_len, sm_scale, part_tokens, workspace,
+                      workspace_bytes, Ws::Caller, stream);
+}
+
+extern "C" int hpa_paged_decode_noalloc(const void* q, void* out, int q_dtype, const void* k_pool,
+                                        const void* v_pool, int kv_dtype, const void* k_scale,
+                                        const void* v_scale, int scale_dtype, const int32_t* block_tables,
+                                        int table_stride, const int32_t* context_lens, int num_seqs,
+                                        int q_per_seq, int num_q_heads, int num_kv_heads, int head_dim,
+                                        int block_size, int num_blocks, int max_context_len,
+                                        float sm_scale, int part_tokens, hipStream_t stream) {
+  return paged_decode(q, out, q_dtype, k_pool, v_pool, kv_dtype, k_scale, v_scale, scale_dtype, block_tables,
+                      table_stride, context_lens, num_seqs, q_per_seq, num_q_heads, num_kv_heads, head_dim,
+                      block_size, num_blocks, max_context_len, sm_scale, part_tokens, nullptr, 0, Ws::Static,
+                      stream);
 }

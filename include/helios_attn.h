@@ -102,6 +102,29 @@ int hpa_paged_decode(const void* q, void* out, int q_dtype, const void* k_pool, 
                      int block_size, int num_blocks, int max_context_len, float sm_scale,
                      int part_tokens, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* Bytes of the static scratch hpa_paged_decode_noalloc uses per GPU. */
+#define HPA_NOALLOC_SCRATCH_BYTES (64u << 20)
+
+/* hpa_paged_decode for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc): the same
+ * arguments and results, with the split-K workspace taken from a static
+ * device array of HPA_NOALLOC_SCRATCH_BYTES that the library holds on each
+ * GPU it runs on until the process ends.  It calls no hipMalloc, hipFree or
+ * allocating routine.  Each call first clears the arrival counters it uses
+ * (a small kernel on `stream`, no memset).  Shapes whose workspace
+ * (hpa_decode_workspace_size) exceeds the scratch are refused with
+ * HPA_ERR_WORKSPACE.  Every call on one GPU shares that GPU's scratch: calls
+ * that may overlap on one GPU (different streams) race and must not be
+ * made.  No counterpart in the reference (helios allocates per call); this
+ * is for the callers above. */
+int hpa_paged_decode_noalloc(const void* q, void* out, int q_dtype, const void* k_pool,
+                             const void* v_pool, int kv_dtype, const void* k_scale,
+                             const void* v_scale, int scale_dtype, const int32_t* block_tables,
+                             int table_stride, const int32_t* context_lens, int num_seqs,
+                             int q_per_seq, int num_q_heads, int num_kv_heads, int head_dim,
+                             int block_size, int num_blocks, int max_context_len, float sm_scale,
+                             int part_tokens, hipStream_t stream);
+
 /* Chunked prefill / verify over a ragged batch, in one launch.
  * Replaces paged_attention_prefill (paged_attn.py:368-408) called once per
  * sequence by BatchedAttention.run (reference exec/model.py:303-317).

@@ -31,8 +31,8 @@ def lib():
 def test_header_declares_the_expected_entry_points():
     assert _declared() == sorted([
         "hpa_version", "hpa_last_error", "hpa_decode_workspace_size", "hpa_paged_decode",
-        "hpa_paged_prefill", "hpa_kv_write", "hpa_kv_write_rope", "hpa_kv_gather",
-        "hpa_copy_blocks", "hpa_step_tables",
+        "hpa_paged_decode_noalloc", "hpa_paged_prefill", "hpa_kv_write", "hpa_kv_write_rope",
+        "hpa_kv_gather", "hpa_copy_blocks", "hpa_step_tables",
     ])
 
 
@@ -53,6 +53,11 @@ def test_status_codes_match_header():
                  "HPA_ERR_LAUNCH", "HPA_F32", "HPA_F16", "HPA_BF16", "HPA_I8"):
         m = re.search(rf"#define {name} (\d+)", text)
         assert int(m.group(1)) == getattr(_lib, name), name
+
+
+def test_noalloc_scratch_size_matches_header():
+    m = re.search(r"#define HPA_NOALLOC_SCRATCH_BYTES \((\d+)u << (\d+)\)", HEADER.read_text())
+    assert int(m.group(1)) << int(m.group(2)) == _lib.HPA_NOALLOC_SCRATCH_BYTES
 
 
 def _ws(waves, rows, D, units):
