@@ -102,11 +102,36 @@ struct TableWindow {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
   }
 
+  // Takes entries [b0, b0 + 128) from an LDS copy made by stage_window.
+  __device__ __forceinline__ void fill_lds(const uint32_t* lds, int b0) {
+    const int lane = threadIdx.x & 63;
+    base = b0;
+    limit = b0 + 128;
+    w0 = lds[lane];
+    w1 = lds[64 + lane];
+  }
+
   __device__ __forceinline__ int get(int lb) const {
     const int i = lb - base;
     return i < 64 ? __builtin_amdgcn_readlane((int)w0, i) : __builtin_amdgcn_readlane((int)w1, i - 64);
   }
 };
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Issues a direct global->LDS copy of table entries [b0, b0 + 128) of `row`
+// (entries at or past `stride` read as 0) into 512 bytes of LDS at `lds`:
+// two loads, no VGPR, nothing waits for them.  The copy has landed once
+// vmcnt has fallen below the number of vector memory instructions issued
+// after it.
+__device__ __forceinline__ void stage_window(void* lds, const int32_t* row, int stride, int b0) {
+  const int lane = threadIdx.x & 63;
+  const int n = max(0, min(stride - b0, 128));
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int32_t*>(row + min(b0, stride)), (short)0, __builtin_amdgcn_readfirstlane(4 * n), 0x00020000);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)lds, 4, 4 * lane, 0, 0, 0);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)((char*)lds + 256), 4, 256 + 4 * lane, 0, 0, 0);
+}
 
 template <class CT, class KVT, class ST, int D, int NT>
 struct AttnCore {
@@ -151,14 +176,18 @@ struct AttnCore {
 
   // Row pointer per n-tile (nullptr for padding rows) and key limit.
   __device__ __forceinline__ void init(const q_t* const* rowq, const int* rowlim) {
+    load_q(rowq);
+    start(rowlim);
+  }
+
+  // Issues the loads of the query rows (the B operand of S^T), one row
+  // pointer per n-tile (nullptr for padding rows).  Nothing waits for them
+  // until start(), so loads issued in between (a table window, the first
+  // K/V steps) are not waited for with them.
+  __device__ __forceinline__ void load_q(const q_t* const* rowq) {
     const int g = lane() >> 4;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      lim[nt] = rowlim[nt];
-      m[nt] = -INFINITY;
-      l[nt] = 0.f;
-#pragma unroll
-      for (int j = 0; j < J; ++j) o[nt][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
       const q_t* p = rowq[nt];
       const bool has = p != nullptr && g * KPL < D;
 #pragma unroll
@@ -178,6 +207,44 @@ struct AttnCore {
           frag_zero(q[nt][c]);
         }
       }
+    }
+  }
+
+  // The query rows from an LDS copy laid out [NT * 16][D] of q_t (row r at
+  // r * D); rows at or past `rows` are zeros.
+  __device__ __forceinline__ void load_q_lds(const uint8_t* lds, int rows) {
+    const int n = lane() & 15, g = lane() >> 4;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int r = nt * 16 + n;
+      const bool has = r < rows && g * KPL < D;
+      const q_t* p = reinterpret_cast<const q_t*>(lds) + (long)(has ? r : 0) * D + (has ? g * KPL : 0);
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        if constexpr (std::is_same<CT, F32>::value) {
+          uint32_t x[8];
+          load_raw<32>(x, p + c * 8);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) q[nt][c].f[e] = has ? __builtin_bit_cast(float, x[e]) : 0.f;
+        } else {
+          uint32_t x[4];
+          load_raw<16>(x, p + c * 8);
+          q[nt][c].w = has ? (u32x4){x[0], x[1], x[2], x[3]} : (u32x4){0, 0, 0, 0};
+        }
+      }
+    }
+  }
+
+  // Resets the softmax state for the rows load_q loaded, with their key
+  // limits, and derives the query terms (this waits for the query rows).
+  __device__ __forceinline__ void start(const int* rowlim) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      lim[nt] = rowlim[nt];
+      m[nt] = -INFINITY;
+      l[nt] = 0.f;
+#pragma unroll
+      for (int j = 0; j < J; ++j) o[nt][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
       if constexpr (I8F16) {
         float sq = 0.f;
 #pragma unroll

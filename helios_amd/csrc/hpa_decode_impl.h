@@ -112,12 +112,27 @@ struct UnitPos {
   long g;      // global position where its cost range starts
 };
 
+// The prologue reads the context lengths once: the first kLocRegs * 64 stay
+// in registers for the search after the total (later ones are read again).
+constexpr int kLocRegs = 4;
+struct LocCache {
+  int c[kLocRegs];
+};
+
 // Cost (steps + kUnitCost per unit) per KV head summed over all sequences
 // (identical in every wave).
-__device__ long total_steps_per_head(const DecodeArgs& a) {
+__device__ long total_steps_per_head(const DecodeArgs& a, LocCache& lc) {
   const int lane = threadIdx.x & 63;
   long acc = 0;
-  for (int base = 0; base < a.num_seqs; base += 256) {
+#pragma unroll
+  for (int i = 0; i < kLocRegs; ++i) {
+    const int b = 64 * i + lane;
+    lc.c[i] = b < a.num_seqs ? a.ctx_lens[b] : 0;
+  }
+#pragma unroll
+  for (int i = 0; i < kLocRegs; ++i)
+    if (64 * i + lane < a.num_seqs) acc += unit_steps(lc.c[i]) + kUnitCost;
+  for (int base = 64 * kLocRegs; base < a.num_seqs; base += 256) {
     int c[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -132,15 +147,17 @@ __device__ long total_steps_per_head(const DecodeArgs& a) {
 }
 
 // The sequence whose cost range in one KV head's position space holds s0
-// (< total).  A sequence's range is kUnitCost positions of overhead followed
-// by its steps.  Wave-uniform result; the caller sets the head.
-__device__ UnitPos locate(const DecodeArgs& a, long s0) {
+// (< total), and its context.  A sequence's range is kUnitCost positions of
+// overhead followed by its steps.  Wave-uniform result; the caller sets the
+// head.
+__device__ UnitPos locate(const DecodeArgs& a, long s0, const LocCache& lc, int& ctx) {
   const int lane = threadIdx.x & 63;
   long run = 0;  // positions before this chunk
   UnitPos p{0, 0, 1, 0};
-  for (int base = 0; base < a.num_seqs; base += 64) {
+  ctx = 0;
+  auto chunk = [&](int base, int cv) -> bool {
     const int b = base + lane;
-    const int n = b < a.num_seqs ? unit_steps(a.ctx_lens[b]) : 0;
+    const int n = b < a.num_seqs ? unit_steps(cv) : 0;
     const long c = b < a.num_seqs ? n + kUnitCost : 0;
     const long incl = wave_incl_scan_l(c);
     const long first = run + incl - c;  // first position of sequence b
@@ -152,9 +169,18 @@ __device__ UnitPos locate(const DecodeArgs& a, long s0) {
       p.b = base + l;
       p.n = __builtin_amdgcn_readfirstlane(__shfl(n, l));
       p.g = uniform_l(__shfl(first, l));
-      return p;
+      ctx = __builtin_amdgcn_readfirstlane(__shfl(clamp_ctx(cv), l));
+      return true;
     }
     run += uniform_l(__shfl(incl, 63));
+    return false;
+  };
+#pragma unroll
+  for (int i = 0; i < kLocRegs; ++i)
+    if (64 * i < a.num_seqs && chunk(64 * i, lc.c[i])) return p;
+  for (int base = 64 * kLocRegs; base < a.num_seqs; base += 64) {
+    const int b = base + lane;
+    if (chunk(base, b < a.num_seqs ? a.ctx_lens[b] : 0)) return p;
   }
   return p;
 }
@@ -168,6 +194,27 @@ constexpr int kCoherent = 16;  // cache-policy bit sc1 (device scope)
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t ws_rsrc(const float* base) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, 0x7fffffff, 0x00020000);
+}
+
+// A wave-uniform element read with a scalar load (through the constant
+// address space), so that it neither takes a VGPR nor joins the vector-load
+// counter: waiting for it never waits for K/V loads in flight.  The array
+// must not change during the kernel.
+__device__ __forceinline__ int uniform_load(const int32_t* p, int i) {
+  return ((const __attribute__((address_space(4))) int32_t*)p)[i];
+}
+
+// Compiler barriers around an explicit wait, so no memory access is moved
+// across it.
+__device__ __forceinline__ void wait_vm_all() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+__device__ __forceinline__ void wait_lgkm_all() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
 template <class CT, class KVT, class ST, int D, int NT, bool BIG>
@@ -190,12 +237,14 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
   const int NG = max(1, a.num_waves / H);
   const int grp = wave / H, head = wave - grp * H;
   if (grp >= NG) return;
-  const long total = uniform_l(total_steps_per_head(a));
+  LocCache lc;
+  const long total = uniform_l(total_steps_per_head(a, lc));
   const long per = max((long)a.min_steps, (total + NG - 1) / NG);
   const long s0 = grp * per;
   if (s0 >= total) return;
   const long s1 = min(total, s0 + per);
-  UnitPos u = locate(a, s0);
+  int ctx = 0;
+  UnitPos u = locate(a, s0, lc, ctx);
   u.kvh = head;
 
   const typename Core::LaneOff lo = Core::lane_off();
@@ -209,48 +258,127 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
     return PoolView{a.k, a.v, a.ks, a.vs, a.tables + (long)uu.b * a.table_stride, a.table_stride,
                     uu.kvh, H, a.bs_log2, a.num_blocks, c};
   };
-  auto unit_ctx = [&](const UnitPos& uu) -> int {
-    return clamp_ctx(__builtin_amdgcn_readfirstlane(a.ctx_lens[uu.b]));
+
+  // Query rows of unit uu, and the key limit of each row for context c.
+  auto row_off = [&](const UnitPos& uu, int r) -> long {
+    const int t = r / G, hh = r - t * G;
+    return ((long)(uu.b * Tq + t) * a.num_q_heads + uu.kvh * G + hh) * D;
+  };
+  auto load_rows = [&](Core& core, const UnitPos& uu) {
+    const q_t* rowq[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int r = nt * 16 + n;
+      rowq[nt] = r < a.rows ? q + row_off(uu, r) : nullptr;
+    }
+    core.load_q(rowq);
   };
 
-  // ---- the first unit: window and the first kDepth steps of loads
+  // ---- per-wave LDS staging.  While a unit streams, the next unit's query
+  // rows and first table window, and the current unit's next table window,
+  // are copied into LDS by direct global->LDS loads: no VGPR holds them and
+  // no wait covers them until they are taken, by which time they have
+  // landed, so neither a unit boundary nor a window refill drains the K/V
+  // loads in flight.
+  constexpr int RB = D * (int)sizeof(q_t);          // bytes of one query row
+  constexpr int QROWB = NT * 16 * RB;
+  constexpr bool kStageQ = QROWB <= 8192;           // larger tiles load rows directly
+  constexpr int QSTAGE = kStageQ ? (QROWB < 1024 ? 1024 : QROWB) : 0;
+  constexpr int WAVE_LDS = QSTAGE + 1024;           // query rows, next unit's window, next window
+  __shared__ __attribute__((aligned(16))) uint8_t lds_all[kWavesPerGroup * WAVE_LDS];
+  uint8_t* const lds_q = lds_all + (threadIdx.x >> 6) * WAVE_LDS;
+  void* const lds_wnext = lds_q + QSTAGE;
+  void* const lds_refill = lds_q + QSTAGE + 512;
+  // rows [0, NT*16) of unit uu as [row][D] q_t; rows past a.rows read as 0
+  auto stage_rows = [&](const UnitPos& uu) {
+    if constexpr (kStageQ) {
+      constexpr int CPR = RB / 16;  // 16-byte chunks per row
+      const int nrec = ((Tq - 1) * a.num_q_heads + G) * RB;
+      const __amdgpu_buffer_rsrc_t rs =
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<q_t*>(q + row_off(uu, 0)), (short)0,
+                                            __builtin_amdgcn_readfirstlane(nrec), 0x00020000);
+#pragma unroll
+      for (int i = 0; i < QSTAGE / 1024; ++i) {
+        const int P = i * 64 + lane, r = P / CPR, c = P % CPR;
+        const int t = r / G, hh = r - t * G;
+        const uint32_t off = r < a.rows ? (uint32_t)((t * a.num_q_heads + hh) * RB + c * 16) : 0xfffffff0u;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(lds_q + i * 1024), 16, off, 0, 0, 0);
+      }
+    }
+  };
+  // one step's loads; with block_size >= 16 the table window moves on by 128
+  // entries when a step passes it, to the copy staged when the current window
+  // was installed (64 or more steps ago: landed, since every later step's
+  // data has been waited for), and the window after it is staged
+  auto advance_window = [&](const PoolView& v, TableWindow& w, int key0, bool enable) {
+    if (enable && key0 < v.ctx && (min(key0 + 31, v.ctx - 1) >> a.bs_log2) >= w.limit) {
+      w.fill_lds(reinterpret_cast<const uint32_t*>(lds_refill), w.limit);
+      wait_lgkm_all();
+      stage_window(lds_refill, v.table, v.table_stride, w.limit);
+    }
+  };
+  auto load_step = [&](const PoolView& v, TableWindow& w, int key0, typename Core::Raw& r, bool enable) {
+    if constexpr (BIG) {
+      advance_window(v, w, key0, enable);
+      Core::load_big(v, w, key0, lo, r, enable);
+    } else {
+      Core::template load_sel<false>(v, w, key0, lo, r, enable);
+    }
+  };
+  auto issue_first = [&](const PoolView& v, TableWindow& w, int first, int end) {
+#pragma unroll
+    for (int k = 0; k < kDepth; ++k) load_step(v, w, 32 * (first + k), rb[k], first + k < end);
+  };
+
+  // ---- the first unit: its query rows and table window through LDS, then
+  // its first kDepth steps of loads
   int lbeg = (int)max(s0 - (u.g + kUnitCost), 0L);  // first local step of the unit in the slice
-  int ctx = unit_ctx(u);
   long sb = u.g + kUnitCost;  // global position of the unit's step 0
   int lend = (int)min((long)u.n, s1 - sb);  // steps of this unit in the slice: [lbeg, lend)
   if (lend <= lbeg) return;  // the slice ends inside the unit's overhead: the next group has it
+  Core core;
   PoolView pv = make_pv(u, ctx);
   TableWindow win;
-  if (BIG && ctx > 0) win.fill(pv.table, pv.table_stride, (32 * lbeg) >> a.bs_log2);  // waited on at first use
-  if (ctx > 0) {
-#pragma unroll
-    for (int k = 0; k < kDepth; ++k)
-      Core::template load_sel<BIG>(pv, win, 32 * (lbeg + k), lo, rb[k], lbeg + k < lend);
+  const int wb0 = (32 * lbeg) >> a.bs_log2;
+  stage_rows(u);
+  if (BIG && ctx > 0) stage_window(lds_wnext, pv.table, pv.table_stride, wb0);
+  wait_vm_all();
+  if constexpr (kStageQ) core.load_q_lds(lds_q, a.rows);
+  else load_rows(core, u);
+  if (BIG && ctx > 0) {
+    win.fill_lds(reinterpret_cast<const uint32_t*>(lds_wnext), wb0);
+    wait_lgkm_all();
+    stage_window(lds_refill, pv.table, pv.table_stride, wb0 + 128);
   }
+  if (ctx > 0) issue_first(pv, win, lbeg, lend);
   bool first_unit = true;
 
   for (;;) {
-    // ---- unit prologue: query rows of (u.b, u.kvh)
-    auto out_row = [&](int r) -> long {
-      const int t = r / G, hh = r - t * G;
-      return ((long)(u.b * Tq + t) * a.num_q_heads + u.kvh * G + hh) * D;
-    };
-    const q_t* rowq[NT];
+    // ---- unit prologue: the query rows (already requested) and row limits
     int rowlim[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       const int r = nt * 16 + n;
-      if (r < a.rows) {
-        rowq[nt] = q + out_row(r);
-        rowlim[nt] = max(ctx - Tq + r / G + 1, 0);
-      } else {
-        rowq[nt] = nullptr;
-        rowlim[nt] = max(ctx, 0);
-      }
+      rowlim[nt] = r < a.rows ? max(ctx - Tq + r / G + 1, 0) : max(ctx, 0);
     }
     const int minlim = max(ctx - Tq + 1, 0);
-    Core core;
-    core.init(rowq, rowlim);
+    core.start(rowlim);
+
+    // ---- what the next unit (the next sequence, same head) needs to start:
+    // its context (a scalar load), its query rows and first table window
+    // (staged in LDS), requested now so that all are in place long before
+    // this unit ends.  The LDS copies of this unit's rows and window were
+    // read (and waited for) before these overwrite them.
+    const bool has_next = sb + lend < s1;
+    int ctx_raw_n = 0;
+    if (has_next) {
+      wait_lgkm_all();  // this unit's rows have left LDS
+      ctx_raw_n = uniform_load(a.ctx_lens, u.b + 1);  // waited for at the boundary
+      UnitPos nx = u;
+      ++nx.b;
+      stage_rows(nx);
+      if (BIG) stage_window(lds_wnext, a.tables + (long)nx.b * a.table_stride, a.table_stride, 0);
+    }
 
     // ---- stream the unit's steps [lbeg, lend); the first kDepth are in flight
     if (ctx > 0) {
@@ -260,8 +388,7 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
         for (int k = 0; k < NB; ++k) {
           if (!done) {
             const int cur = st + k;
-            Core::template load_sel<BIG>(pv, win, 32 * (cur + kDepth), lo, rb[(k + kDepth) % NB],
-                                         cur + kDepth < lend);
+            load_step(pv, win, 32 * (cur + kDepth), rb[(k + kDepth) % NB], cur + kDepth < lend);
             core.compute(rb[k], 32 * cur, a.scale_log2, 32 * cur + 32 > minlim, ctx);
             done = cur + 1 >= lend;
           }
@@ -269,152 +396,201 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
       }
     }
 
-    // ---- the next unit (the next sequence, same head), started before this
-    // unit's epilogue so that its loads overlap the epilogue's latency
-    const bool has_next = sb + lend < s1;
+    // ---- the next unit's query rows, window and first kDepth steps of loads
+    // go out before this unit's epilogue, so they overlap its latency.  The
+    // loads still in flight are this unit's trailing empty prefetches and
+    // its staged copies, long landed: waiting for them costs little.
+    wait_vm_all();
     UnitPos un = u;
     int ctx_n = 0, lend_n = 0;
-    TableWindow win_n;
     if (has_next) {
       un.g += u.n + kUnitCost;
       ++un.b;
-      un.n = unit_steps(__builtin_amdgcn_readfirstlane(a.ctx_lens[un.b]));
-      ctx_n = unit_ctx(un);
+      un.n = unit_steps(ctx_raw_n);
+      ctx_n = clamp_ctx(ctx_raw_n);
       lend_n = (int)min((long)un.n, s1 - (un.g + kUnitCost));
-      if (BIG && ctx_n > 0 && lend_n > 0) win_n.fill(a.tables + (long)un.b * a.table_stride, a.table_stride, 0);
     }
+    const bool go_next = has_next && lend_n > 0;
     const PoolView pv_n = make_pv(un, ctx_n);
-    auto prime_next = [&]() {
-      if (has_next && ctx_n > 0 && lend_n > 0) {
-#pragma unroll
-        for (int k = 0; k < kDepth; ++k)
-          Core::template load_sel<BIG>(pv_n, win_n, 32 * k, lo, rb[k], k < lend_n);
-      }
-    };
-
-    // ---- unit epilogue
     float lrow[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) lrow[nt] = core.row_l(nt);
-    bool finish = lbeg == 0 && lend == u.n;  // the whole unit is in this slice
-    if (!finish) {
-      // publish this piece, then count it in
-      const long slot = 2L * wave + (first_unit ? 0 : 1);
-      const __amdgpu_buffer_rsrc_t ro = ws_rsrc(a.ws_o), rml = ws_rsrc(a.ws_ml);
+    TableWindow win_n;
+    if (go_next) {
+      // the epilogue below reads o, m and l, not the query rows
+      if constexpr (kStageQ) core.load_q_lds(lds_q, a.rows);
+      else load_rows(core, un);
+      if (BIG) win_n.fill_lds(reinterpret_cast<const uint32_t*>(lds_wnext), 0);
+      wait_lgkm_all();
+      if (BIG && ctx_n > 0) stage_window(lds_refill, pv_n.table, pv_n.table_stride, 128);
+      if (ctx_n > 0) issue_first(pv_n, win_n, 0, lend_n);
+    }
+
+    // ---- output rows: the lane holds the 4J contiguous dims [4Jg, 4Jg + 4J)
+    // of row r (element (j, i) of the accumulators at J*i + j), stored in
+    // 16-byte pieces
+    auto store_row = [&](const UnitPos& uu, int r, const float* vals, float inv) {
+      if (4 * J * g >= D) return;  // head_dim below 16: lanes past it hold nothing
+      q_t* orow = out + row_off(uu, r) + 4 * J * g;
+      if constexpr (sizeof(q_t) == 2) {
+        uint32_t w[2 * J];
+#pragma unroll
+        for (int k = 0; k < 2 * J; ++k)
+          w[k] = (uint32_t)Cvt<CT>::from_f32(vals[2 * k] * inv) | ((uint32_t)Cvt<CT>::from_f32(vals[2 * k + 1] * inv) << 16);
+        if constexpr (2 * J >= 4) {
+#pragma unroll
+          for (int c = 0; c < 2 * J / 4; ++c)
+            *reinterpret_cast<u32x4*>(orow + 8 * c) = (u32x4){w[4 * c], w[4 * c + 1], w[4 * c + 2], w[4 * c + 3]};
+        } else {
+          *reinterpret_cast<u32x2*>(orow) = (u32x2){w[0], w[1]};
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < J; ++c)
+          *reinterpret_cast<f32x4*>(orow + 4 * c) =
+              (f32x4){vals[4 * c] * inv, vals[4 * c + 1] * inv, vals[4 * c + 2] * inv, vals[4 * c + 3] * inv};
+      }
+    };
+    // Merges the pieces of unit uu (held by groups wa_..wb_; group p's in
+    // the slots of wave p H + head, group wa_'s first or second slot per
+    // slot_a_) in piece order and stores its output rows.  This wave's own
+    // piece comes from its registers -- the exact values it would have
+    // stored -- and every other from the workspace, so the result does not
+    // depend on which wave merges.
+    const __amdgpu_buffer_rsrc_t ro = ws_rsrc(a.ws_o), rml = ws_rsrc(a.ws_ml);
+    auto merge_pieces = [&](const UnitPos& uu, int wa_, int wb_, long slot_a_) {
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         const int r = nt * 16 + n;
-        if (r < a.rows) {
-          // the lane's 4J dims are contiguous from 4Jg, element (j, i) at J*i + j
-          float tmp[4 * J];
+        if (r >= a.rows) continue;
+        float own[4 * J];
 #pragma unroll
-          for (int j = 0; j < J; ++j)
+        for (int j = 0; j < J; ++j)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) tmp[J * i + j] = core.out_val(nt, j, i);
-          const uint32_t ob = (uint32_t)(((slot * a.rows + r) * D + 4 * J * g) * 4);
+          for (int i = 0; i < 4; ++i) own[J * i + j] = core.out_val(nt, j, i);
+        // running merge over pieces in order: (M, L, acc) rescaled as each
+        // piece's (m, l, O) arrives
+        float M = -INFINITY, L = 0.f;
+        float acc[4 * J];
 #pragma unroll
-          for (int c = 0; c < J; ++c)
-            if (4 * J * g + 4 * c < D)
-              __builtin_amdgcn_raw_buffer_store_b128(
-                  (u32x4){__builtin_bit_cast(uint32_t, tmp[4 * c]), __builtin_bit_cast(uint32_t, tmp[4 * c + 1]),
-                          __builtin_bit_cast(uint32_t, tmp[4 * c + 2]), __builtin_bit_cast(uint32_t, tmp[4 * c + 3])},
-                  ro, ob + 16 * c, 0, kCoherent);
-          if (g == 0)
-            __builtin_amdgcn_raw_buffer_store_b64(
-                (u32x2){__builtin_bit_cast(uint32_t, core.m[nt]), __builtin_bit_cast(uint32_t, lrow[nt])}, rml,
-                (uint32_t)((slot * a.rows + r) * 8), 0, kCoherent);
+        for (int e = 0; e < 4 * J; ++e) acc[e] = 0.f;
+#pragma unroll 2
+        for (int p = wa_; p <= wb_; ++p) {
+          float mp, lp, val[4 * J];
+          if (p == grp) {
+            mp = core.m[nt];
+            lp = lrow[nt];
+#pragma unroll
+            for (int e = 0; e < 4 * J; ++e) val[e] = own[e];
+          } else {
+            const long sl = p == wa_ ? slot_a_ : 2L * (p * H + head);
+            const u32x2 ml = __builtin_amdgcn_raw_buffer_load_b64(rml, (uint32_t)((sl * a.rows + r) * 8), 0, kCoherent);
+            const uint32_t ob = (uint32_t)(((sl * a.rows + r) * D + 4 * J * g) * 4);
+#pragma unroll
+            for (int c = 0; c < J; ++c) {
+              const u32x4 ov = 4 * J * g + 4 * c < D
+                                   ? __builtin_amdgcn_raw_buffer_load_b128(ro, ob + 16 * c, 0, kCoherent)
+                                   : (u32x4){0, 0, 0, 0};
+              // elements are copied out before bit_cast: a bit_cast applied to
+              // an ext_vector element reads element 0 (hipcc 7.2)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const uint32_t oe = ov[e];
+                val[4 * c + e] = __builtin_bit_cast(float, oe);
+              }
+            }
+            const uint32_t m0 = ml[0], l0 = ml[1];
+            mp = __builtin_bit_cast(float, m0);
+            lp = __builtin_bit_cast(float, l0);
+          }
+          const float Mn = fmaxf(M, mp);
+          const float Mref = Mn == -INFINITY ? 0.f : Mn;
+          const float sa = __builtin_amdgcn_exp2f(M - Mref), sp = __builtin_amdgcn_exp2f(mp - Mref);
+          L = __builtin_fmaf(L, sa, lp * sp);
+#pragma unroll
+          for (int e = 0; e < 4 * J; ++e) acc[e] = __builtin_fmaf(acc[e], sa, val[e] * sp);
+          M = Mn;
         }
+        store_row(uu, r, acc, L > 0.f ? 1.f / L : 0.f);
       }
+    };
+
+
+    // ---- unit epilogue
+    const bool finish = lbeg == 0 && lend == u.n;  // the whole unit is in this slice
+    if (!finish) {
+      // A piece of a unit cut by slice boundaries.  Group p's piece sits in
+      // the slots of wave p H + head; group wa, whose slice ends in the unit,
+      // saw the unit first iff its slice began inside the unit's range.
       const int wa = (int)(sb / per), wb = (int)((sb + u.n - 1) / per);  // groups holding the pieces
       const int unit = u.b * H + u.kvh;
-      // the piece's stores are complete (hence visible device-wide) before
-      // the counter moves
-      __atomic_signal_fence(__ATOMIC_SEQ_CST);
-      __builtin_amdgcn_s_waitcnt(0);
-      __atomic_signal_fence(__ATOMIC_SEQ_CST);
-      int old = 0;
-      if (lane == 0) old = __hip_atomic_fetch_add(a.counters + unit, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      // the next unit's loads go out while the count comes back
-      prime_next();
-      old = __builtin_amdgcn_readfirstlane(old);
-      if (old == wb - wa) {
-        // last piece: merge every piece in piece order, all read back from
-        // the workspace (this wave's own included), so every merging wave
-        // evaluates the same expression
-        if (lane == 0) __hip_atomic_store(a.counters + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        // group wa saw this unit first iff its slice began inside the unit's
-        // range; the piece of group p sits in the slots of wave p H + head
-        const long slot_a = 2L * (wa * H + head) + ((long)wa * per >= u.g ? 0 : 1);
+      const long slot = 2L * wave + (first_unit ? 0 : 1);
+      const long slot_a = 2L * (wa * H + head) + ((long)wa * per >= u.g ? 0 : 1);
+      // The piece of group wa holds the unit's first steps, streamed at the
+      // end of its slice, while the others streamed theirs at the start of
+      // theirs: wa is usually the last to finish.  It first reads the count;
+      // if every other piece is in, it merges at once from its own registers
+      // and never publishes.
+      bool merge = false;
+      if (grp == wa) {
+        int seen = 0;
+        if (lane == 0) seen = __hip_atomic_load(a.counters + unit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        merge = __builtin_amdgcn_readfirstlane(seen) == wb - wa;
+      }
+      if (!merge) {
+        // publish this piece
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
           const int r = nt * 16 + n;
-          if (r >= a.rows) continue;
-          // running merge over pieces in order: (M, L, acc) rescaled as each
-          // piece's (m, l, O) arrives
-          float M = -INFINITY, L = 0.f;
-          float acc[4 * J];
+          if (r < a.rows) {
+            // the lane's 4J dims are contiguous from 4Jg, element (j, i) at J*i + j
+            float tmp[4 * J];
 #pragma unroll
-          for (int e = 0; e < 4 * J; ++e) acc[e] = 0.f;
-#pragma unroll 2
-          for (int p = wa; p <= wb; ++p) {
-            const long sl = p == wa ? slot_a : 2L * (p * H + head);
-            const u32x2 ml = __builtin_amdgcn_raw_buffer_load_b64(rml, (uint32_t)((sl * a.rows + r) * 8), 0, kCoherent);
-            const uint32_t ob = (uint32_t)(((sl * a.rows + r) * D + 4 * J * g) * 4);
-            u32x4 ov[J];
+            for (int j = 0; j < J; ++j)
+#pragma unroll
+              for (int i = 0; i < 4; ++i) tmp[J * i + j] = core.out_val(nt, j, i);
+            const uint32_t ob = (uint32_t)(((slot * a.rows + r) * D + 4 * J * g) * 4);
 #pragma unroll
             for (int c = 0; c < J; ++c)
-              ov[c] = 4 * J * g + 4 * c < D
-                          ? __builtin_amdgcn_raw_buffer_load_b128(ro, ob + 16 * c, 0, kCoherent)
-                          : (u32x4){0, 0, 0, 0};
-            // elements are copied out before bit_cast: a bit_cast applied to an
-            // ext_vector element reads element 0 (hipcc 7.2)
-            const uint32_t m0 = ml[0], l0 = ml[1];
-            const float mp = __builtin_bit_cast(float, m0), lp = __builtin_bit_cast(float, l0);
-            const float Mn = fmaxf(M, mp);
-            const float Mref = Mn == -INFINITY ? 0.f : Mn;
-            const float sa = __builtin_amdgcn_exp2f(M - Mref), sb = __builtin_amdgcn_exp2f(mp - Mref);
-            L = L * sa + lp * sb;
-#pragma unroll
-            for (int c = 0; c < J; ++c)
-#pragma unroll
-              for (int e = 0; e < 4; ++e)
-              {
-                const uint32_t oe = ov[c][e];
-                acc[4 * c + e] = acc[4 * c + e] * sa + __builtin_bit_cast(float, oe) * sb;
-              }
-            M = Mn;
+              if (4 * J * g + 4 * c < D)
+                __builtin_amdgcn_raw_buffer_store_b128(
+                    (u32x4){__builtin_bit_cast(uint32_t, tmp[4 * c]), __builtin_bit_cast(uint32_t, tmp[4 * c + 1]),
+                            __builtin_bit_cast(uint32_t, tmp[4 * c + 2]), __builtin_bit_cast(uint32_t, tmp[4 * c + 3])},
+                    ro, ob + 16 * c, 0, kCoherent);
+            if (g == 0)
+              __builtin_amdgcn_raw_buffer_store_b64(
+                  (u32x2){__builtin_bit_cast(uint32_t, core.m[nt]), __builtin_bit_cast(uint32_t, lrow[nt])}, rml,
+                  (uint32_t)((slot * a.rows + r) * 8), 0, kCoherent);
           }
-          const float inv = L > 0.f ? 1.f / L : 0.f;
-          q_t* orow = out + out_row(r);
-#pragma unroll
-          for (int j = 0; j < J; ++j)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const int d = Core::out_dim(g, j, i);
-              if (d < D) orow[d] = Cvt<CT>::from_f32(acc[J * i + j] * inv);
-            }
         }
+        // count it in once its stores are complete (hence visible device-wide)
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_waitcnt(0);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        int old = 0;
+        if (lane == 0) old = __hip_atomic_fetch_add(a.counters + unit, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        merge = __builtin_amdgcn_readfirstlane(old) == wb - wa;
+      }
+      if (merge) {
+        if (lane == 0) __hip_atomic_store(a.counters + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        merge_pieces(u, wa, wb, slot_a);
       }
     } else {
-      prime_next();
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         const int r = nt * 16 + n;
         if (r < a.rows) {
-          const float inv = lrow[nt] > 0.f ? 1.f / lrow[nt] : 0.f;
-          q_t* orow = out + out_row(r);
+          float vals[4 * J];
 #pragma unroll
           for (int j = 0; j < J; ++j)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const int d = Core::out_dim(g, j, i);
-              if (d < D) orow[d] = Cvt<CT>::from_f32(ctx > 0 ? core.out_val(nt, j, i) * inv : 0.f);
-            }
+            for (int i = 0; i < 4; ++i) vals[J * i + j] = ctx > 0 ? core.out_val(nt, j, i) : 0.f;
+          store_row(u, r, vals, lrow[nt] > 0.f ? 1.f / lrow[nt] : 0.f);
         }
       }
     }
 
-    if (!has_next || lend_n <= 0) break;
+    if (!go_next) break;
     u = un;
     ctx = ctx_n;
     sb = un.g + kUnitCost;
