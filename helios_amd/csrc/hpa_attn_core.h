@@ -210,31 +210,6 @@ struct AttnCore {
     }
   }
 
-  // The query rows from an LDS copy laid out [NT * 16][D] of q_t (row r at
-  // r * D); rows at or past `rows` are zeros.
-  __device__ __forceinline__ void load_q_lds(const uint8_t* lds, int rows) {
-    const int n = lane() & 15, g = lane() >> 4;
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      const int r = nt * 16 + n;
-      const bool has = r < rows && g * KPL < D;
-      const q_t* p = reinterpret_cast<const q_t*>(lds) + (long)(has ? r : 0) * D + (has ? g * KPL : 0);
-#pragma unroll
-      for (int c = 0; c < C; ++c) {
-        if constexpr (std::is_same<CT, F32>::value) {
-          uint32_t x[8];
-          load_raw<32>(x, p + c * 8);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) q[nt][c].f[e] = has ? __builtin_bit_cast(float, x[e]) : 0.f;
-        } else {
-          uint32_t x[4];
-          load_raw<16>(x, p + c * 8);
-          q[nt][c].w = has ? (u32x4){x[0], x[1], x[2], x[3]} : (u32x4){0, 0, 0, 0};
-        }
-      }
-    }
-  }
-
   // Resets the softmax state for the rows load_q loaded, with their key
   // limits, and derives the query terms (this waits for the query rows).
   __device__ __forceinline__ void start(const int* rowlim) {

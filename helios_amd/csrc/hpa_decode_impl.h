@@ -191,6 +191,9 @@ __device__ UnitPos locate(const DecodeArgs& a, long s0, const LocCache& lc, int&
 // the device's coherence point, so publishing a piece needs only a wait for
 // its stores to complete, not a device-wide cache write-back.
 constexpr int kCoherent = 16;  // cache-policy bit sc1 (device scope)
+// A buffer offset past every buffer's records (ws_rsrc sets 0x7fffffff): a
+// load from it returns zeros without touching memory.
+constexpr uint32_t kPastRecords = 0x80000000u;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t ws_rsrc(const float* base) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, 0x7fffffff, 0x00020000);
@@ -222,6 +225,7 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
   typedef AttnCore<CT, KVT, ST, D, NT> Core;
   typedef typename CT::storage q_t;
   constexpr int J = Core::J;
+  constexpr int kMergeBatch = J <= 4 ? 4 : 2;  // split-K pieces loaded per round trip of a merge
   const int wave = __builtin_amdgcn_readfirstlane(blockIdx.x * kWavesPerGroup + (threadIdx.x >> 6));
   if (wave >= a.num_waves) return;
   const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
@@ -274,38 +278,16 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
     core.load_q(rowq);
   };
 
-  // ---- per-wave LDS staging.  While a unit streams, the next unit's query
-  // rows and first table window, and the current unit's next table window,
-  // are copied into LDS by direct global->LDS loads: no VGPR holds them and
-  // no wait covers them until they are taken, by which time they have
-  // landed, so neither a unit boundary nor a window refill drains the K/V
-  // loads in flight.
-  constexpr int RB = D * (int)sizeof(q_t);          // bytes of one query row
-  constexpr int QROWB = NT * 16 * RB;
-  constexpr bool kStageQ = QROWB <= 8192;           // larger tiles load rows directly
-  constexpr int QSTAGE = kStageQ ? (QROWB < 1024 ? 1024 : QROWB) : 0;
-  constexpr int WAVE_LDS = QSTAGE + 1024;           // query rows, next unit's window, next window
-  __shared__ __attribute__((aligned(16))) uint8_t lds_all[kWavesPerGroup * WAVE_LDS];
-  uint8_t* const lds_q = lds_all + (threadIdx.x >> 6) * WAVE_LDS;
-  void* const lds_wnext = lds_q + QSTAGE;
-  void* const lds_refill = lds_q + QSTAGE + 512;
-  // rows [0, NT*16) of unit uu as [row][D] q_t; rows past a.rows read as 0
-  auto stage_rows = [&](const UnitPos& uu) {
-    if constexpr (kStageQ) {
-      constexpr int CPR = RB / 16;  // 16-byte chunks per row
-      const int nrec = ((Tq - 1) * a.num_q_heads + G) * RB;
-      const __amdgpu_buffer_rsrc_t rs =
-          __builtin_amdgcn_make_buffer_rsrc(const_cast<q_t*>(q + row_off(uu, 0)), (short)0,
-                                            __builtin_amdgcn_readfirstlane(nrec), 0x00020000);
-#pragma unroll
-      for (int i = 0; i < QSTAGE / 1024; ++i) {
-        const int P = i * 64 + lane, r = P / CPR, c = P % CPR;
-        const int t = r / G, hh = r - t * G;
-        const uint32_t off = r < a.rows ? (uint32_t)((t * a.num_q_heads + hh) * RB + c * 16) : 0xfffffff0u;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(lds_q + i * 1024), 16, off, 0, 0, 0);
-      }
-    }
-  };
+  // ---- per-wave LDS staging of table windows.  While a unit streams, the
+  // next unit's first table window and the current unit's next window are
+  // copied into LDS by direct global->LDS loads: no VGPR holds them and no
+  // wait covers them until they are taken, by which time they have landed,
+  // so neither a unit boundary nor a window refill waits for a table read
+  // with K/V loads in flight.  (Query rows need no staging: loaded before a
+  // unit's first K/V steps, they arrive with them.)
+  __shared__ __attribute__((aligned(16))) uint32_t lds_windows[kWavesPerGroup][2][128];
+  void* const lds_wnext = lds_windows[threadIdx.x >> 6][0];
+  void* const lds_refill = lds_windows[threadIdx.x >> 6][1];
   // one step's loads; with block_size >= 16 the table window moves on by 128
   // entries when a step passes it, to the copy staged when the current window
   // was installed (64 or more steps ago: landed, since every later step's
@@ -330,24 +312,20 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
     for (int k = 0; k < kDepth; ++k) load_step(v, w, 32 * (first + k), rb[k], first + k < end);
   };
 
-  // ---- the first unit: its query rows and table window through LDS, then
-  // its first kDepth steps of loads
+  // ---- the first unit: its query rows, its table window, then its first
+  // kDepth steps of loads (in that order: waiting for the rows does not wait
+  // for the K/V steps behind them)
   int lbeg = (int)max(s0 - (u.g + kUnitCost), 0L);  // first local step of the unit in the slice
   long sb = u.g + kUnitCost;  // global position of the unit's step 0
   int lend = (int)min((long)u.n, s1 - sb);  // steps of this unit in the slice: [lbeg, lend)
   if (lend <= lbeg) return;  // the slice ends inside the unit's overhead: the next group has it
   Core core;
+  load_rows(core, u);
   PoolView pv = make_pv(u, ctx);
   TableWindow win;
   const int wb0 = (32 * lbeg) >> a.bs_log2;
-  stage_rows(u);
-  if (BIG && ctx > 0) stage_window(lds_wnext, pv.table, pv.table_stride, wb0);
-  wait_vm_all();
-  if constexpr (kStageQ) core.load_q_lds(lds_q, a.rows);
-  else load_rows(core, u);
   if (BIG && ctx > 0) {
-    win.fill_lds(reinterpret_cast<const uint32_t*>(lds_wnext), wb0);
-    wait_lgkm_all();
+    win.fill(pv.table, pv.table_stride, wb0);
     stage_window(lds_refill, pv.table, pv.table_stride, wb0 + 128);
   }
   if (ctx > 0) issue_first(pv, win, lbeg, lend);
@@ -365,19 +343,15 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
     core.start(rowlim);
 
     // ---- what the next unit (the next sequence, same head) needs to start:
-    // its context (a scalar load), its query rows and first table window
-    // (staged in LDS), requested now so that all are in place long before
-    // this unit ends.  The LDS copies of this unit's rows and window were
-    // read (and waited for) before these overwrite them.
+    // its context (a scalar load) and first table window (staged in LDS),
+    // requested now so that both are in place long before this unit ends.
+    // The LDS copy of this unit's window was read (and waited for) before
+    // this one overwrites it.
     const bool has_next = sb + lend < s1;
     int ctx_raw_n = 0;
     if (has_next) {
-      wait_lgkm_all();  // this unit's rows have left LDS
       ctx_raw_n = uniform_load(a.ctx_lens, u.b + 1);  // waited for at the boundary
-      UnitPos nx = u;
-      ++nx.b;
-      stage_rows(nx);
-      if (BIG) stage_window(lds_wnext, a.tables + (long)nx.b * a.table_stride, a.table_stride, 0);
+      if (BIG) stage_window(lds_wnext, a.tables + (long)(u.b + 1) * a.table_stride, a.table_stride, 0);
     }
 
     // ---- stream the unit's steps [lbeg, lend); the first kDepth are in flight
@@ -399,7 +373,7 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
     // ---- the next unit's query rows, window and first kDepth steps of loads
     // go out before this unit's epilogue, so they overlap its latency.  The
     // loads still in flight are this unit's trailing empty prefetches and
-    // its staged copies, long landed: waiting for them costs little.
+    // its staged window, long landed: waiting for them costs little.
     wait_vm_all();
     UnitPos un = u;
     int ctx_n = 0, lend_n = 0;
@@ -417,9 +391,7 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
     for (int nt = 0; nt < NT; ++nt) lrow[nt] = core.row_l(nt);
     TableWindow win_n;
     if (go_next) {
-      // the epilogue below reads o, m and l, not the query rows
-      if constexpr (kStageQ) core.load_q_lds(lds_q, a.rows);
-      else load_rows(core, un);
+      load_rows(core, un);  // the epilogue below reads o, m and l, not the query rows
       if (BIG) win_n.fill_lds(reinterpret_cast<const uint32_t*>(lds_wnext), 0);
       wait_lgkm_all();
       if (BIG && ctx_n > 0) stage_window(lds_refill, pv_n.table, pv_n.table_stride, 128);
@@ -474,42 +446,60 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
         float acc[4 * J];
 #pragma unroll
         for (int e = 0; e < 4 * J; ++e) acc[e] = 0.f;
-#pragma unroll 2
-        for (int p = wa_; p <= wb_; ++p) {
-          float mp, lp, val[4 * J];
-          if (p == grp) {
-            mp = core.m[nt];
-            lp = lrow[nt];
+        // pieces go in batches of kMergeBatch: a batch's loads are all issued
+        // before its first piece is merged, so a unit cut into P pieces
+        // waits ceil(P / kMergeBatch) round trips, not P
+        for (int p0 = wa_; p0 <= wb_; p0 += kMergeBatch) {
+          u32x2 ml[kMergeBatch];
+          u32x4 ov[kMergeBatch][J];
 #pragma unroll
-            for (int e = 0; e < 4 * J; ++e) val[e] = own[e];
-          } else {
+          for (int k = 0; k < kMergeBatch; ++k) {
+            const int p = p0 + k;
+            // this wave's own piece, and pieces past wb_, read nothing: an
+            // offset past the buffer's records returns zeros
+            const bool ld = p <= wb_ && p != grp;
             const long sl = p == wa_ ? slot_a_ : 2L * (p * H + head);
-            const u32x2 ml = __builtin_amdgcn_raw_buffer_load_b64(rml, (uint32_t)((sl * a.rows + r) * 8), 0, kCoherent);
+            ml[k] = __builtin_amdgcn_raw_buffer_load_b64(rml, ld ? (uint32_t)((sl * a.rows + r) * 8) : kPastRecords,
+                                                         0, kCoherent);
             const uint32_t ob = (uint32_t)(((sl * a.rows + r) * D + 4 * J * g) * 4);
 #pragma unroll
-            for (int c = 0; c < J; ++c) {
-              const u32x4 ov = 4 * J * g + 4 * c < D
-                                   ? __builtin_amdgcn_raw_buffer_load_b128(ro, ob + 16 * c, 0, kCoherent)
-                                   : (u32x4){0, 0, 0, 0};
-              // elements are copied out before bit_cast: a bit_cast applied to
-              // an ext_vector element reads element 0 (hipcc 7.2)
-#pragma unroll
-              for (int e = 0; e < 4; ++e) {
-                const uint32_t oe = ov[e];
-                val[4 * c + e] = __builtin_bit_cast(float, oe);
-              }
-            }
-            const uint32_t m0 = ml[0], l0 = ml[1];
-            mp = __builtin_bit_cast(float, m0);
-            lp = __builtin_bit_cast(float, l0);
+            for (int c = 0; c < J; ++c)
+              ov[k][c] = 4 * J * g + 4 * c < D
+                             ? __builtin_amdgcn_raw_buffer_load_b128(ro, ld ? ob + 16 * c : kPastRecords, 0, kCoherent)
+                             : (u32x4){0, 0, 0, 0};
           }
-          const float Mn = fmaxf(M, mp);
-          const float Mref = Mn == -INFINITY ? 0.f : Mn;
-          const float sa = __builtin_amdgcn_exp2f(M - Mref), sp = __builtin_amdgcn_exp2f(mp - Mref);
-          L = __builtin_fmaf(L, sa, lp * sp);
 #pragma unroll
-          for (int e = 0; e < 4 * J; ++e) acc[e] = __builtin_fmaf(acc[e], sa, val[e] * sp);
-          M = Mn;
+          for (int k = 0; k < kMergeBatch; ++k) {
+            const int p = p0 + k;
+            if (p > wb_) break;
+            float mp, lp, val[4 * J];
+            if (p == grp) {
+              mp = core.m[nt];
+              lp = lrow[nt];
+#pragma unroll
+              for (int e = 0; e < 4 * J; ++e) val[e] = own[e];
+            } else {
+              // elements are copied out before bit_cast: a bit_cast applied
+              // to an ext_vector element reads element 0 (hipcc 7.2)
+#pragma unroll
+              for (int c = 0; c < J; ++c)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                  const uint32_t oe = ov[k][c][e];
+                  val[4 * c + e] = __builtin_bit_cast(float, oe);
+                }
+              const uint32_t m0 = ml[k][0], l0 = ml[k][1];
+              mp = __builtin_bit_cast(float, m0);
+              lp = __builtin_bit_cast(float, l0);
+            }
+            const float Mn = fmaxf(M, mp);
+            const float Mref = Mn == -INFINITY ? 0.f : Mn;
+            const float sa = __builtin_amdgcn_exp2f(M - Mref), sp = __builtin_amdgcn_exp2f(mp - Mref);
+            L = __builtin_fmaf(L, sa, lp * sp);
+#pragma unroll
+            for (int e = 0; e < 4 * J; ++e) acc[e] = __builtin_fmaf(acc[e], sa, val[e] * sp);
+            M = Mn;
+          }
         }
         store_row(uu, r, acc, L > 0.f ? 1.f / L : 0.f);
       }
@@ -526,13 +516,14 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
       const int unit = u.b * H + u.kvh;
       const long slot = 2L * wave + (first_unit ? 0 : 1);
       const long slot_a = 2L * (wa * H + head) + ((long)wa * per >= u.g ? 0 : 1);
-      // The piece of group wa holds the unit's first steps, streamed at the
-      // end of its slice, while the others streamed theirs at the start of
-      // theirs: wa is usually the last to finish.  It first reads the count;
-      // if every other piece is in, it merges at once from its own registers
-      // and never publishes.
+      // With two pieces, group wa's holds the unit's first steps, streamed at
+      // the end of its slice, while group wb streamed the rest at the start
+      // of its own: wa is almost always the last to finish.  It first reads
+      // the count; if the other piece is in, it merges at once from its own
+      // registers and never publishes.  (With more pieces the middle ones
+      // span whole slices and end with wa's, so the read rarely pays.)
       bool merge = false;
-      if (grp == wa) {
+      if (grp == wa && wb == wa + 1) {
         int seen = 0;
         if (lane == 0) seen = __hip_atomic_load(a.counters + unit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         merge = __builtin_amdgcn_readfirstlane(seen) == wb - wa;
