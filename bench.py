@@ -354,10 +354,12 @@ def cpu_baseline(wl, budget_s):
 def time_steps(wl, steps, warmup, warmup_s):
     """`warmup` untimed steps, continued until at least `warmup_s` seconds
     have passed (the GPU clock needs tens of milliseconds of sustained work
-    to ramp up), then exactly `steps` timed steps, each bracketed by its own
-    pair of HIP events on the stream the kernels run on (torch's current
-    stream).  Returns (median ms, mean ms, warmup steps run, seconds of the
-    timed region by the host clock)."""
+    to ramp up), then exactly `steps` timed steps between one pair of HIP
+    events on the stream the kernels run on (torch's current stream), with a
+    synchronisation on both sides.  The host enqueues ahead of the GPU, so
+    the elapsed time is the steps' back-to-back GPU time (per-step event
+    pairs would add host time between small steps).  Returns (ms per step,
+    warmup steps run, seconds of the timed region by the host clock)."""
     import torch
 
     stream = torch.cuda.current_stream()
@@ -368,17 +370,15 @@ def time_steps(wl, steps, warmup, warmup_s):
         if done % 50 == 0:
             torch.cuda.synchronize()
     torch.cuda.synchronize()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t_wall = time.perf_counter()
-    for e0, e1 in ev:
-        e0.record(stream)
+    e0.record(stream)
+    for _ in range(steps):
         wl.step()
-        e1.record(stream)
+    e1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t_wall
-    ms = sorted(e0.elapsed_time(e1) for e0, e1 in ev)
-    med = ms[len(ms) // 2] if len(ms) % 2 else 0.5 * (ms[len(ms) // 2 - 1] + ms[len(ms) // 2])
-    return med, sum(ms) / len(ms), done, wall
+    return e0.elapsed_time(e1) / steps, done, wall
 
 
 def roofline(wl, ms, key):
@@ -717,10 +717,10 @@ def main():
         wl = DecodeWorkload(args.config, device, seed, args.part_tokens, copies)
 
     print(f"bench: {wl.name} built; timing {args.steps} steps", file=sys.stderr, flush=True)
-    med, mean, warm_done, wall = time_steps(wl, args.steps, args.warmup, args.warmup_s)
-    print(f"bench: {med * 1e3:.1f} us per step (median); CPU baseline next", file=sys.stderr, flush=True)
+    ms_step, warm_done, wall = time_steps(wl, args.steps, args.warmup, args.warmup_s)
+    print(f"bench: {ms_step * 1e3:.1f} us per step; CPU baseline next", file=sys.stderr, flush=True)
     key = f"config{args.config}" + ("_int8" if args.kv_int8 else "")
-    value = wl.tokens / (med * 1e-3)
+    value = wl.tokens / (ms_step * 1e-3)
     cpu = cpu_baseline(wl, args.cpu_budget) if args.cpu_budget > 0 else None
 
     line = {
@@ -733,9 +733,8 @@ def main():
         "warmup": args.warmup,
         "warmup_s": args.warmup_s,
         "warmup_steps_run": warm_done,
-        "ms_per_step": round(med, 5),
-        "ms_per_step_mean": round(mean, 5),
-        "timing": "median of per-step HIP event pairs on the kernels' stream",
+        "ms_per_step": round(ms_step, 5),
+        "timing": "one HIP event pair around the timed steps on the kernels' stream, divided by steps",
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -743,7 +742,7 @@ def main():
         ("f32" if args.config == 1 else "f16"),
         "data": "synthetic (seeded N(0,1); int8 KV quantized on the GPU by the library's write kernel)",
         "config": wl.config(),
-        "roofline": roofline(wl, med, key),
+        "roofline": roofline(wl, ms_step, key),
         "cpu_baseline": cpu,
         "wall_s_timed_region": round(wall, 4),
     }
@@ -751,14 +750,14 @@ def main():
         # config 4 (the MFMA-bound chunked prefill) measured in the same run
         pw = PrefillWorkload(device, 3)
         print(f"bench: {pw.name} built; timing {args.steps} steps", file=sys.stderr, flush=True)
-        pmed, pmean, pwarm, _ = time_steps(pw, args.steps, args.warmup, args.warmup_s)
-        print(f"bench: {pmed * 1e3:.1f} us per step (median); CPU baseline next", file=sys.stderr, flush=True)
+        pms, pwarm, _ = time_steps(pw, args.steps, args.warmup, args.warmup_s)
+        print(f"bench: {pms * 1e3:.1f} us per step; CPU baseline next", file=sys.stderr, flush=True)
         line["prefill"] = {
             "metric": "paged-attn chunked-prefill tokens/s + MFMA TFLOP/s (% peak) on 1 MI355X",
-            "value": round(pw.tokens / (pmed * 1e-3), 1), "unit": "tokens/s",
-            "ms_per_step": round(pmed, 5), "ms_per_step_mean": round(pmean, 5),
+            "value": round(pw.tokens / (pms * 1e-3), 1), "unit": "tokens/s",
+            "ms_per_step": round(pms, 5),
             "warmup_steps_run": pwarm, "dtype": "f16", "config": pw.config(),
-            "roofline": roofline(pw, pmed, "config4"),
+            "roofline": roofline(pw, pms, "config4"),
             "cpu_baseline": cpu_baseline(pw, args.cpu_budget) if args.cpu_budget > 0 else None,
         }
     print(json.dumps(line))
