@@ -351,15 +351,20 @@ def cpu_baseline(wl, budget_s):
             "seconds": round(secs, 2)}
 
 
-def time_steps(wl, steps, warmup, warmup_s):
+def time_steps(wl, steps, warmup, warmup_s, chunk=10):
     """`warmup` untimed steps, continued until at least `warmup_s` seconds
     have passed (the GPU clock needs tens of milliseconds of sustained work
-    to ramp up), then exactly `steps` timed steps between one pair of HIP
-    events on the stream the kernels run on (torch's current stream), with a
-    synchronisation on both sides.  The host enqueues ahead of the GPU, so
-    the elapsed time is the steps' back-to-back GPU time (per-step event
-    pairs would add host time between small steps).  Returns (ms per step,
-    warmup steps run, seconds of the timed region by the host clock)."""
+    to ramp up), then exactly `steps` timed steps with a synchronisation on
+    both sides.  The steps are timed in chunks of `chunk`, each between its
+    own pair of HIP events on the stream the kernels run on (torch's current
+    stream): an event record between every two steps costs the GPU time of
+    its own (config 4 reads ~8% slower with one around every step).  The
+    host enqueues faster than the GPU runs even config 2's 25 us steps, so
+    the steps run back to back.  (Holding the stream with a spin kernel
+    while the host enqueued them let the clock drop: config 4 read 8%
+    slower.)  Returns (median over
+    the chunks of ms per step, ms per step from the first start to the last
+    end, warmup steps run, seconds of the timed region by the host clock)."""
     import torch
 
     stream = torch.cuda.current_stream()
@@ -370,15 +375,19 @@ def time_steps(wl, steps, warmup, warmup_s):
         if done % 50 == 0:
             torch.cuda.synchronize()
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    sizes = [min(chunk, steps - i) for i in range(0, steps, chunk)]
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in sizes]
     t_wall = time.perf_counter()
-    e0.record(stream)
-    for _ in range(steps):
-        wl.step()
-    e1.record(stream)
+    for (e0, e1), n in zip(ev, sizes):
+        e0.record(stream)
+        for _ in range(n):
+            wl.step()
+        e1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t_wall
-    return e0.elapsed_time(e1) / steps, done, wall
+    per = sorted(e0.elapsed_time(e1) / n for (e0, e1), n in zip(ev, sizes))
+    med = per[len(per) // 2] if len(per) % 2 else 0.5 * (per[len(per) // 2 - 1] + per[len(per) // 2])
+    return med, ev[0][0].elapsed_time(ev[-1][1]) / steps, done, wall
 
 
 def roofline(wl, ms, key):
@@ -717,7 +726,7 @@ def main():
         wl = DecodeWorkload(args.config, device, seed, args.part_tokens, copies)
 
     print(f"bench: {wl.name} built; timing {args.steps} steps", file=sys.stderr, flush=True)
-    ms_step, warm_done, wall = time_steps(wl, args.steps, args.warmup, args.warmup_s)
+    ms_step, ms_run, warm_done, wall = time_steps(wl, args.steps, args.warmup, args.warmup_s)
     print(f"bench: {ms_step * 1e3:.1f} us per step; CPU baseline next", file=sys.stderr, flush=True)
     key = f"config{args.config}" + ("_int8" if args.kv_int8 else "")
     value = wl.tokens / (ms_step * 1e-3)
@@ -734,7 +743,9 @@ def main():
         "warmup_s": args.warmup_s,
         "warmup_steps_run": warm_done,
         "ms_per_step": round(ms_step, 5),
-        "timing": "one HIP event pair around the timed steps on the kernels' stream, divided by steps",
+        "ms_per_step_run": round(ms_run, 5),
+        "timing": "median over chunks of 10 steps, each chunk between its own HIP event pair on the kernels' "
+                  "stream; ms_per_step_run = first start to last end / steps",
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -750,12 +761,12 @@ def main():
         # config 4 (the MFMA-bound chunked prefill) measured in the same run
         pw = PrefillWorkload(device, 3)
         print(f"bench: {pw.name} built; timing {args.steps} steps", file=sys.stderr, flush=True)
-        pms, pwarm, _ = time_steps(pw, args.steps, args.warmup, args.warmup_s)
+        pms, pms_run, pwarm, _ = time_steps(pw, args.steps, args.warmup, args.warmup_s)
         print(f"bench: {pms * 1e3:.1f} us per step; CPU baseline next", file=sys.stderr, flush=True)
         line["prefill"] = {
             "metric": "paged-attn chunked-prefill tokens/s + MFMA TFLOP/s (% peak) on 1 MI355X",
             "value": round(pw.tokens / (pms * 1e-3), 1), "unit": "tokens/s",
-            "ms_per_step": round(pms, 5),
+            "ms_per_step": round(pms, 5), "ms_per_step_run": round(pms_run, 5),
             "warmup_steps_run": pwarm, "dtype": "f16", "config": pw.config(),
             "roofline": roofline(pw, pms, "config4"),
             "cpu_baseline": cpu_baseline(pw, args.cpu_budget) if args.cpu_budget > 0 else None,
