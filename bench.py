@@ -336,8 +336,8 @@ def _cpu_model():
 
 def cpu_baseline(wl, budget_s):
     """The oracle's restatement of helios' CPU route on a bounded sample,
-    with every core this process may run on (BASELINE.md's rule: n =
-    len(sched_getaffinity)) given to the BLAS pool."""
+    with every core this process may run on (n = len(sched_getaffinity))
+    given to the BLAS pool."""
     n = len(os.sched_getaffinity(0))
     try:
         from threadpoolctl import threadpool_limits
@@ -357,14 +357,14 @@ def time_steps(wl, steps, warmup, warmup_s, chunk=10):
     to ramp up), then exactly `steps` timed steps with a synchronisation on
     both sides.  The steps are timed in chunks of `chunk`, each between its
     own pair of HIP events on the stream the kernels run on (torch's current
-    stream): an event record between every two steps costs the GPU time of
-    its own (config 4 reads ~8% slower with one around every step).  The
-    host enqueues faster than the GPU runs even config 2's 25 us steps, so
-    the steps run back to back.  (Holding the stream with a spin kernel
-    while the host enqueued them let the clock drop: config 4 read 8%
-    slower.)  Returns (median over
-    the chunks of ms per step, ms per step from the first start to the last
-    end, warmup steps run, seconds of the timed region by the host clock)."""
+    stream), and the result is the median over the chunks.  An event record
+    between every two steps costs GPU time of its own (config 4 reads ~8%
+    slower with one around every step).  The host enqueues faster than the
+    GPU runs even config 2's 25 us steps, so the steps run back to back.
+    (Holding the stream with a spin kernel while the host enqueued them let
+    the clock drop: config 4 read 8% slower.)  Returns (median over the
+    chunks of ms per step, ms per step from the first start to the last end,
+    warmup steps run, seconds of the timed region by the host clock)."""
     import torch
 
     stream = torch.cuda.current_stream()
