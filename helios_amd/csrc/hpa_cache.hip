@@ -111,19 +111,26 @@ __device__ __forceinline__ float wave_max(float x) {
 
 // int8 pool: one wave per (token, KV head) and tensor (K or V).  Lane l owns
 // head_dim elements [l*EPL, l*EPL + EPL).
-template <class IT, class ST, int EPL>
-__device__ __forceinline__ void quant_one(const typename IT::storage* x, int8_t* qdst,
-                                          typename ST::storage* sdst, int D, const float* cs_row = nullptr,
-                                          const float* sn_row = nullptr) {
+// One (token, head) row into registers: the lane's EPL values, rotated when
+// cs_row is given.
+template <class IT, int EPL>
+__device__ __forceinline__ void load_row(const typename IT::storage* x, int D, const float* cs_row,
+                                         const float* sn_row, float* v) {
   const int lane = threadIdx.x & 63;
-  float v[EPL];
-  float amax = 0.f;
 #pragma unroll
   for (int e = 0; e < EPL; ++e) {
     const int d = lane * EPL + e;
     v[e] = d < D ? (cs_row ? rope_elem<IT>(x, d, D, cs_row, sn_row) : Cvt<IT>::to_f32(x[d])) : 0.f;
-    amax = fmaxf(amax, fabsf(v[e]));
   }
+}
+
+// helios' _quantize of one row held in registers, stored at qdst / sdst
+template <class ST, int EPL>
+__device__ __forceinline__ void quant_store(const float* v, int8_t* qdst, typename ST::storage* sdst, int D) {
+  const int lane = threadIdx.x & 63;
+  float amax = 0.f;
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) amax = fmaxf(amax, fabsf(v[e]));
   amax = wave_max(amax);
   const float s = fmaxf(amax, 1e-8f) / 127.0f;
 #pragma unroll
@@ -152,19 +159,23 @@ __global__ __launch_bounds__(256) void kv_write_i8_kernel(const WriteArgs a) {
   const int item = blockIdx.x * 4 + (threadIdx.x >> 6);  // (token, head)
   if (item >= nt * H) return;
   const int i = item / H, h = item - i * H;
-  const long slot = write_slot(a, b, i, h);
-  if (slot < 0) return;
   typedef typename IT::storage i_t;
   typedef typename ST::storage s_t;
+  // the rows are read before the slot is known, so these loads and the
+  // block-table read are in flight together; a row whose slot turns out
+  // invalid is dropped (its rotary rows are read only when they exist)
   const long src = ((long)(t0 + i) * H + h) * D;
-  const long row = (long)(a.start_pos[b] + i) * (D >> 1);
-  quant_one<IT, ST, EPL>(reinterpret_cast<const i_t*>(a.k) + src,
-                         reinterpret_cast<int8_t*>(a.kp) + slot * D,
-                         reinterpret_cast<s_t*>(a.ks) + slot, D, a.rope_cos ? a.rope_cos + row : nullptr,
-                         a.rope_cos ? a.rope_sin + row : nullptr);
-  quant_one<IT, ST, EPL>(reinterpret_cast<const i_t*>(a.v) + src,
-                         reinterpret_cast<int8_t*>(a.vp) + slot * D,
-                         reinterpret_cast<s_t*>(a.vs) + slot, D);
+  const int pos = a.start_pos[b] + i;
+  const bool rot = a.rope_cos != nullptr && pos >= 0 && pos < a.rope_rows;
+  const long row = (long)pos * (D >> 1);
+  float kx[EPL], vx[EPL];
+  load_row<IT, EPL>(reinterpret_cast<const i_t*>(a.k) + src, D, rot ? a.rope_cos + row : nullptr,
+                    rot ? a.rope_sin + row : nullptr, kx);
+  load_row<IT, EPL>(reinterpret_cast<const i_t*>(a.v) + src, D, nullptr, nullptr, vx);
+  const long slot = write_slot(a, b, i, h);
+  if (slot < 0) return;
+  quant_store<ST, EPL>(kx, reinterpret_cast<int8_t*>(a.kp) + slot * D, reinterpret_cast<s_t*>(a.ks) + slot, D);
+  quant_store<ST, EPL>(vx, reinterpret_cast<int8_t*>(a.vp) + slot * D, reinterpret_cast<s_t*>(a.vs) + slot, D);
 }
 
 // ------------------------------------------------------------------- gather
