@@ -163,6 +163,8 @@ static int paged_decode(const void* q, void* out, int q_dtype, const void* k_poo
     pa.num_blocks = num_blocks;
     pa.scale_log2 = sm_scale * 1.4426950408889634f;
     pa.uniform_q = q_per_seq;
+    if (nt == 4 && launch_verify_i8(pa, q_dtype, kv_dtype, scale_dtype, head_dim, stream))
+      return check_launch("hpa_paged_decode");
     if (launch_prefill_mfma(pa, q_dtype, kv_dtype, scale_dtype, head_dim, q_per_seq, stream))
       return check_launch("hpa_paged_decode");
     if (nt == 0) {

@@ -56,6 +56,12 @@ __device__ __forceinline__ SeqSpan seq_span(const PrefillArgs& a, int b) {
 bool launch_prefill_mfma(const PrefillArgs& a, int q_dtype, int kv_dtype, int scale_dtype, int head_dim,
                          int max_q_len, hipStream_t s);
 
+// A verify (uniform_q > 0) of 33-64 rows per KV head over an int8 pool
+// (fp16 queries, fp16 / fp32 scales, head_dim 64 / 128, block_size >= 16),
+// dequantised in registers (hpa_verify_i8.hip); returns false (launching
+// nothing) for other shapes.
+bool launch_verify_i8(const PrefillArgs& a, int q_dtype, int kv_dtype, int scale_dtype, int head_dim, hipStream_t s);
+
 // The generic prefill kernel (any supported dtype, head_dim and block size);
 // returns HPA_OK or an HPA_ERR_* status (with its message) for shapes it
 // has no kernel for.

@@ -187,17 +187,64 @@ def test_wide_verify_runs_the_mfma_prefill_kernel(Hq, Hkv, T, D, dtype, quant):
     (start = context - T), and the oracle.  On int8 pools that kernel attends
     over the dequantised values rounded to the compute dtype, as helios'
     gather hands them over (paged_attn.py:213-235), so the oracle reads the
-    same values."""
+    same values.  fp16 queries over int8 pools take the register-dequantising
+    verify kernel instead (test_int8_wide_verify_dequantises_in_registers)."""
     print(f"wide verify {Hq}/{Hkv}x{T} D {D} {dtype} int8 {quant}", flush=True)
     lens = [T, T + 5, 40, 129, 300]
     cache, tables, q = _case(80 + Hq + T, len(lens), lens, Hq, Hkv, D, 16, dtype,
                              quant=quant, q_per_seq=T)
     got = paged_attention_verify_batched(q, cache, tables, lens, T)
-    same = paged_attention_varlen(q, cache, tables, [T] * len(lens), [c - T for c in lens], lens)
-    assert torch.equal(got, same)
+    if quant and dtype == torch.float16:
+        # the verify kernel keeps the dequantised values in fp32, as the
+        # decode kernel does; both oracles agree with it to the bound
+        _check(got, _oracle_decode(cache, q, tables, lens, q_per_seq=T), dtype, "int8 wide verify")
+    else:
+        same = paged_attention_varlen(q, cache, tables, [T] * len(lens), [c - T for c in lens], lens)
+        assert torch.equal(got, same)
     pool = pool_dequantized(cache) if quant else pool_of(cache)
     want = R.paged_verify_batched(to_np(q).astype(np.float32), pool, tables, lens, T)
     _check(got, want, dtype, "wide verify")
+
+
+@pytest.mark.parametrize("scale_dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("Hq,Hkv,T,D", [(8, 1, 5, 128), (32, 4, 8, 128), (14, 2, 5, 64), (16, 2, 7, 64),
+                                        (32, 8, 16, 128)])
+def test_int8_wide_verify_dequantises_in_registers(Hq, Hkv, T, D, scale_dtype):
+    """33-64 rows per KV head, fp16 queries over an int8 pool: the verify
+    kernel that turns each wave's own int8 operands into fp16 in registers
+    (1152 + x, offsets removed algebraically) against the oracle on the
+    exactly dequantised values.  Contexts cover a context equal to the token
+    count, steps ending mid-block and mid-step, one 16-key half of a step
+    past the context, and tables longer than 128 blocks.  Two calls give
+    the same bits."""
+    print(f"int8 verify in registers: {Hq}/{Hkv} x {T}, D {D}, scales {scale_dtype}", flush=True)
+    lens = [T, T + 1, 33, 48, 64 + T, 300, 2100 + T]
+    cache, tables, q = _case(140 + Hq + T + D, len(lens), lens, Hq, Hkv, D, 16, torch.float16,
+                             quant=True, scale_dtype=scale_dtype, q_per_seq=T)
+    got = paged_attention_verify_batched(q, cache, tables, lens, T)
+    torch.cuda.synchronize()
+    _check(got, _oracle_decode(cache, q, tables, lens, q_per_seq=T), torch.float16, "int8 verify in registers")
+    again = paged_attention_verify_batched(q, cache, tables, lens, T)
+    assert torch.equal(got, again)
+
+
+def test_int8_wide_verify_many_sequences_and_scale_range():
+    """Config 5's head shape with 12 speculative tokens (48 rows per KV
+    head) over 300 sequences, so workgroups run longest-first over several
+    rounds, with key scales from 2^-14 to 2^4 and value scales from 2^-14
+    to 2^-6 on different blocks (values stay below 2, where fp16 rounds the
+    output within the bound)."""
+    print("int8 verify in registers: 300 sequences", flush=True)
+    rng = np.random.default_rng(150)
+    T = 12
+    lens = [int(x) for x in rng.integers(T, 1500, size=300)]
+    cache, tables, q = _case(150, len(lens), lens, 32, 8, 128, 16, torch.float16, quant=True, q_per_seq=T)
+    gen = torch.Generator(device="cuda").manual_seed(151)
+    for sc, top in ((cache.k_scale, 5), (cache.v_scale, -5)):
+        e = torch.randint(-14, top, (sc.shape[0], 1, 1), generator=gen, device="cuda").float()
+        sc.copy_((torch.rand(sc.shape, generator=gen, device="cuda") * 0.5 + 0.5) * torch.exp2(e))
+    got = paged_attention_verify_batched(q, cache, tables, lens, T)
+    _check(got, _oracle_decode(cache, q, tables, lens, q_per_seq=T), torch.float16, "int8 verify, 300 sequences")
 
 
 @pytest.mark.parametrize("D,bs,dtype", [(128, 8, torch.float16), (32, 16, torch.float16),
