@@ -156,11 +156,18 @@ struct AttnCore {
     uint32_t vs[2][SW];
   };
 
-  // int8 KV with fp16 compute converts a byte x to the fp16 value 1152 + x
-  // (two VALU ops per pair of values instead of three) and removes the
-  // offset algebraically: S = S' - 1152 * sum(q) and O = O' - 1152 * sum(P').
+  // int8 KV with fp16 compute converts a key byte x to the fp16 subnormal
+  // (128 + x) 2^-24 and a value byte to the fp16 value 1152 + x (two VALU
+  // ops per pair of values instead of three) and removes the offsets
+  // algebraically: S = 2^24 (S' - 128 2^-24 sum(q)) and O = O' - 1152 sum(P').
+  // The small key offset keeps the fp32 sums of S' near the score's own
+  // magnitude, so large key scales do not amplify their rounding.
   static constexpr bool I8F16 = QUANT && std::is_same<CT, F16>::value;
-  static constexpr float kI8Off = 1152.f;
+  static constexpr float kI8KOff = 0x1p-17f;  // 128 * 2^-24
+  static constexpr float kI8VOff = 1152.f;
+  // P enters the PV MFMAs as two terms (hi + lo) for bf16 compute and for
+  // int8 pools with fp16 compute
+  static constexpr bool kSplitP = std::is_same<CT, BF16>::value || I8F16;
   // Rescale the accumulators only when a row max grows by more than 2^8;
   // probabilities then stay below 2^8 relative to the running reference.
   static constexpr float kLazy = 8.f;
@@ -168,7 +175,7 @@ struct AttnCore {
   Frag<CT> q[NT][C];
   f32x4 o[NT][J];
   f32x4 ps[NT];     // I8F16: sum over keys of the fp16 P' fed to the PV MFMAs
-  float qoff[NT];   // I8F16: 1152 * sum_d q[row][d]
+  float qoff[NT];   // I8F16: 128 * 2^-24 * sum_d q[row][d]
   float m[NT], l[NT];
   int lim[NT];
 
@@ -232,7 +239,7 @@ struct AttnCore {
             const f16x2 h = __builtin_bit_cast(f16x2, wi);
             sq += (float)h[0] + (float)h[1];
           }
-        qoff[nt] = kI8Off * xor_sum(sq);
+        qoff[nt] = kI8KOff * xor_sum(sq);
         ps[nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
       }
     }
@@ -442,12 +449,12 @@ struct AttnCore {
     if constexpr (QUANT) {
       const uint32_t w0 = kr[2 * c], w1 = kr[2 * c + 1];
       if constexpr (std::is_same<CT, F16>::value) {
-        // [b0^0x80, 0x64, b1^0x80, 0x64] = fp16 (1152 + x0, 1152 + x1)
+        // [b0^0x80, 0x00, b1^0x80, 0x00] = fp16 ((128 + x0) 2^-24, (128 + x1) 2^-24)
         const uint32_t x0 = w0 ^ 0x80808080u, x1 = w1 ^ 0x80808080u;
-        f.w[0] = __builtin_amdgcn_perm(0x64646464u, x0, 0x04010400u);
-        f.w[1] = __builtin_amdgcn_perm(0x64646464u, x0, 0x04030402u);
-        f.w[2] = __builtin_amdgcn_perm(0x64646464u, x1, 0x04010400u);
-        f.w[3] = __builtin_amdgcn_perm(0x64646464u, x1, 0x04030402u);
+        f.w[0] = __builtin_amdgcn_perm(0u, x0, 0x0C010C00u);
+        f.w[1] = __builtin_amdgcn_perm(0u, x0, 0x0C030C02u);
+        f.w[2] = __builtin_amdgcn_perm(0u, x1, 0x0C010C00u);
+        f.w[3] = __builtin_amdgcn_perm(0u, x1, 0x0C030C02u);
       } else {
         float x[8];
 #pragma unroll
@@ -548,7 +555,7 @@ struct AttnCore {
     // fragment at a time (each converted once and used by every n-tile), so
     // at most one converted V fragment is live
     Frag<CT> pf[NT];
-    Frag<CT> pl[NT];  // bf16 only: the low half of P
+    Frag<CT> pl[NT];  // bf16 and int8 -> fp16: the low half of P
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       float x[8];
@@ -557,7 +564,7 @@ struct AttnCore {
       for (int s = 0; s < 8; ++s) {
         float v = st[s >> 2][nt][s & 3];
         if constexpr (I8F16) v -= qoff[nt];
-        v *= scale_log2 * scale_at(r.ks[s >> 2], s & 3);
+        v *= (I8F16 ? scale_log2 * 0x1p24f : scale_log2) * scale_at(r.ks[s >> 2], s & 3);
         if (masked) {
           const int key = k0 + 16 * (s >> 2) + 4 * g + (s & 3);
           v = key < lim[nt] ? v : -INFINITY;
@@ -589,19 +596,25 @@ struct AttnCore {
       }
       l[nt] += psum;
       frag_from_f32(pf[nt], x);
-      if constexpr (std::is_same<CT, BF16>::value) {
-        // bf16 keeps 8 significant bits; P = hi + lo with both halves in
-        // bf16 carries ~16, so probabilities are not the error term.
+      if constexpr (kSplitP) {
+        // bf16 keeps 8 significant bits, fp16 11: P = hi + lo with both
+        // halves in the compute type carries twice that, so the rounding of
+        // the weights is not the error term.  (On int8 pools P holds the
+        // value scale, P * vs, whose per-key rounding would otherwise reach
+        // the output undamped.)
         float lo[8];
 #pragma unroll
-        for (int s = 0; s < 8; ++s)
-          lo[s] = x[s] - bf16_bits_to_f32((pf[nt].w[s >> 1] >> (16 * (s & 1))) & 0xffffu);
+        for (int s = 0; s < 8; ++s) {
+          const uint32_t hb = (pf[nt].w[s >> 1] >> (16 * (s & 1))) & 0xffffu;
+          lo[s] = x[s] - (std::is_same<CT, BF16>::value ? bf16_bits_to_f32(hb) : f16_bits_to_f32(hb));
+        }
         frag_from_f32(pl[nt], lo);
       }
       if constexpr (I8F16) {
         Frag<CT> ones;
         ones.w = (u32x4){0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u};
         ps[nt] = mma(ones, pf[nt], ps[nt]);
+        ps[nt] = mma(ones, pl[nt], ps[nt]);
       }
     }
 #pragma unroll
@@ -611,14 +624,14 @@ struct AttnCore {
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         o[nt][j] = mma(vf, pf[nt], o[nt][j]);
-        if constexpr (std::is_same<CT, BF16>::value) o[nt][j] = mma(vf, pl[nt], o[nt][j]);
+        if constexpr (kSplitP) o[nt][j] = mma(vf, pl[nt], o[nt][j]);
       }
     }
   }
 
   // Accumulator element (j, i) of n-tile nt with the int8 offset removed.
   __device__ __forceinline__ float out_val(int nt, int j, int i) const {
-    if constexpr (I8F16) return o[nt][j][i] - kI8Off * ps[nt][0];
+    if constexpr (I8F16) return o[nt][j][i] - kI8VOff * ps[nt][0];
     return o[nt][j][i];
   }
 

@@ -165,6 +165,52 @@ def test_int8_kv(scale_dtype, D, dtype):
     _check(got, _oracle_decode(cache, q, tables, lens), dtype, f"int8 D={D}")
 
 
+def _scale_range(cache, seed):
+    """Key scales from 2^-14 to 2^4 and value scales from 2^-14 to 2^-6,
+    drawn per block (the payload keeps its bytes)."""
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    for sc, top in ((cache.k_scale, 5), (cache.v_scale, -5)):
+        e = torch.randint(-14, top, (sc.shape[0], 1, 1), generator=gen, device="cuda").float()
+        sc.copy_((torch.rand(sc.shape, generator=gen, device="cuda") * 0.5 + 0.5) * torch.exp2(e))
+
+
+@pytest.mark.parametrize("scale_dtype", [torch.float16, torch.float32])
+def test_int8_decode_few_keys_large_values(scale_dtype):
+    """400 contexts of 1-5 keys with value scales doubled (values up to ~8):
+    with so few keys no rounding of a single weight averages out, so fp16
+    weights P * vs would leave up to 2^-11 |v| in the output.  Outputs below
+    4 in magnitude (where rounding the output itself costs <= 2^-12 * 4)
+    stay within 2e-3; larger ones within 2e-3 plus their own half-ulp."""
+    print(f"int8 decode, 1-5 keys, scales {scale_dtype}", flush=True)
+    rng = np.random.default_rng(7)
+    lens = [int(x) for x in rng.integers(1, 6, size=400)]
+    cache, tables, q = _case(9, len(lens), lens, 32, 8, 128, 16, torch.float16, quant=True,
+                             scale_dtype=scale_dtype)
+    cache.v_scale.mul_(2.0)
+    got = to_np(paged_attention_decode_batched(q, cache, tables, lens)).astype(np.float64)
+    want = _oracle_decode(cache, q, tables, lens)
+    err = np.abs(got - want)
+    small = np.abs(want) < 4
+    assert err[small].max() <= 2e-3, f"|out| < 4: max-abs {err[small].max():.3e}"
+    assert (err <= 2e-3 + np.abs(want) * 2.0 ** -11).all(), f"max-abs {err.max():.3e}"
+
+
+@pytest.mark.parametrize("scale_dtype", [torch.float16, torch.float32])
+def test_int8_decode_scale_range(scale_dtype):
+    """300 contexts up to 1500 keys with key scales up to 2^4: scores reach
+    thousands, so an offset in the fp16 key operand that is large next to
+    the key bytes would leave its fp32 rounding, times the scale, in the
+    softmax weights."""
+    print(f"int8 decode, scale range, scales {scale_dtype}", flush=True)
+    rng = np.random.default_rng(150)
+    lens = [int(x) for x in rng.integers(1, 1500, size=300)]
+    cache, tables, q = _case(150, len(lens), lens, 32, 8, 128, 16, torch.float16, quant=True,
+                             scale_dtype=scale_dtype)
+    _scale_range(cache, 151)
+    got = paged_attention_decode_batched(q, cache, tables, lens)
+    _check(got, _oracle_decode(cache, q, tables, lens), torch.float16, "int8 decode, scale range")
+
+
 @pytest.mark.parametrize("Hq,Hkv,T", [(32, 8, 3), (14, 2, 1), (14, 2, 3), (8, 1, 5), (16, 1, 4), (2, 2, 2)])
 @pytest.mark.parametrize("quant", [False, True])
 def test_verify_rows_and_gqa_groups(Hq, Hkv, T, quant):
@@ -239,10 +285,7 @@ def test_int8_wide_verify_many_sequences_and_scale_range():
     T = 12
     lens = [int(x) for x in rng.integers(T, 1500, size=300)]
     cache, tables, q = _case(150, len(lens), lens, 32, 8, 128, 16, torch.float16, quant=True, q_per_seq=T)
-    gen = torch.Generator(device="cuda").manual_seed(151)
-    for sc, top in ((cache.k_scale, 5), (cache.v_scale, -5)):
-        e = torch.randint(-14, top, (sc.shape[0], 1, 1), generator=gen, device="cuda").float()
-        sc.copy_((torch.rand(sc.shape, generator=gen, device="cuda") * 0.5 + 0.5) * torch.exp2(e))
+    _scale_range(cache, 151)
     got = paged_attention_verify_batched(q, cache, tables, lens, T)
     _check(got, _oracle_decode(cache, q, tables, lens, q_per_seq=T), torch.float16, "int8 verify, 300 sequences")
 
