@@ -50,6 +50,35 @@ __device__ __forceinline__ SeqSpan seq_span(const PrefillArgs& a, int b) {
   return sp;
 }
 
+// Longest-first order within an XCD: workgroup 8 m + x (x = its XCD) runs
+// the item of rank m by cost among the nk items 8 j + x.  An item's key
+// packs its cost above its inverted index j, so keys are distinct (ties go
+// to the lower j) and the ranks a permutation; a rank counts the larger
+// keys, four per LDS read.  keys: LDS for nk rounded up to 4 ints, 16-byte
+// aligned; pick: one LDS int.  Every thread of the workgroup calls it; the
+// result is uniform.  nk <= kLptMax; cost(j) >= 0.
+constexpr int kLptBits = 9;
+constexpr int kLptMax = 1 << kLptBits;
+template <int NTHREADS, class F>
+__device__ __forceinline__ int lpt_pick(int* keys, int* pick, int nk, int m, int xcd, F cost) {
+  const int nk4 = (nk + 3) & ~3;
+  for (int j = threadIdx.x; j < nk4; j += NTHREADS)
+    keys[j] = j < nk ? (min(cost(j), (1 << (30 - kLptBits)) - 1) << kLptBits) | (kLptMax - 1 - j) : -1;
+  __syncthreads();
+  for (int j = threadIdx.x; j < nk; j += NTHREADS) {
+    const int kj = keys[j];
+    int rank = 0;
+#pragma unroll 4
+    for (int i = 0; i < nk4; i += 4) {
+      const int4 c = *reinterpret_cast<const int4*>(&keys[i]);
+      rank += (c.x > kj) + (c.y > kj) + (c.z > kj) + (c.w > kj);
+    }
+    if (rank == m) *pick = 8 * j + xcd;
+  }
+  __syncthreads();
+  return __builtin_amdgcn_readfirstlane(*pick);
+}
+
 // LDS-tiled 32x32 MFMA prefill for fp16 / bf16 queries over pools of the
 // same dtype or int8 pools (fp16 / fp32 scales), head_dim 64 or 128 and
 // block_size >= 16; returns false (launching nothing) for other shapes.

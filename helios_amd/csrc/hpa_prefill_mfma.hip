@@ -134,7 +134,6 @@ __device__ __forceinline__ constexpr int v_swz(int nch, int row) {
   return nch == 16 ? (row & 3) * 4 + ((row & 2) ? 2 : 0) : (row & 3) * 2;
 }
 
-constexpr int kPfLptMax = 512;           // items per XCD up to which workgroups run longest-first
 
 // Work item i is the (i / units)-th heaviest row tile of unit i % units.
 // Workgroups go to the 8 XCDs round-robin by id and, within an XCD, start in
@@ -222,22 +221,9 @@ __global__ __launch_bounds__(64 * kPfWaves, 2) void prefill_mfma_kernel(const Pr
     int& s_pick = *reinterpret_cast<int*>(&smem[SMEM - 4]);
     const int xcd = item & 7, m = item >> 3;
     const int nk = ((int)gridDim.x - xcd + 7) >> 3;  // items on this XCD
-    if (nk <= kPfLptMax) {
-      int* cost = reinterpret_cast<int*>(&smem[0]);
-      for (int j = threadIdx.x; j < nk; j += 64 * kPfWaves) cost[j] = item_cost(a, 8 * j + xcd, units, tiles_per_unit);
-      __syncthreads();
-      for (int j = threadIdx.x; j < nk; j += 64 * kPfWaves) {
-        const int cj = cost[j];
-        int rank = 0;
-        for (int i = 0; i < nk; ++i) {
-          const int ci = cost[i];
-          rank += (ci > cj) | ((ci == cj) & (i < j));
-        }
-        if (rank == m) s_pick = 8 * j + xcd;
-      }
-      __syncthreads();
-      item = __builtin_amdgcn_readfirstlane(s_pick);  // uniform: keeps everything below scalar
-    }
+    if (nk <= kLptMax)
+      item = lpt_pick<64 * kPfWaves>(reinterpret_cast<int*>(&smem[0]), &s_pick, nk, m, xcd,
+                                     [&](int j) { return item_cost(a, 8 * j + xcd, units, tiles_per_unit); });
   }
   const int unit = item % units;
   const int tile = tiles_per_unit - 1 - item / units;

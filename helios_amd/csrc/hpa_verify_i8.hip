@@ -45,8 +45,6 @@ typedef float f32x16v __attribute__((ext_vector_type(16)));
 
 constexpr int kViWaves = 2;    // 32 rows each
 constexpr int kViStages = 4;   // LDS stages; copies run kViStages - 1 steps ahead
-constexpr int kViLptBits = 9;
-constexpr int kViLptMax = 1 << kViLptBits;  // units per XCD up to which workgroups run longest-first
 // rescale only when a row max grows by more than 2^kViLazy, so P <= 16 and
 // P * vs stays inside fp16 for every scale of an fp16-range value (vs < 517)
 constexpr int kViLazy = 4;
@@ -173,37 +171,14 @@ __global__ __launch_bounds__(64 * kViWaves, 2) void verify_i8_kernel(const Prefi
   const int units = a.num_seqs * a.num_kv_heads;
   const int T = a.uniform_q, G = a.group, H = a.num_kv_heads;
 
-  // ---- which unit this workgroup runs: longest-first per XCD (the
-  // workgroup with id 8m + x takes the m-th longest unit among 8j + x).  A
-  // unit's key packs its context above its inverted index, so keys are
-  // distinct (ties go to the lower index) and the ranks a permutation; a
-  // rank counts the larger keys, four per LDS read, so the pick takes a
-  // few microseconds rather than a serial read per unit.
+  // ---- which unit this workgroup runs: longest-first per XCD
   int unit = (int)blockIdx.x;
   {
-    const int xcd = unit & 7, m = unit >> 3;
+    const int xcd = unit & 7;
     const int nk = ((int)gridDim.x - xcd + 7) >> 3;
-    if (nk <= kViLptMax) {
-      int* key = reinterpret_cast<int*>(&smem[0]);
-      const int nk4 = (nk + 3) & ~3;
-      for (int j = threadIdx.x; j < nk4; j += 64 * kViWaves) {
-        const int c = j < nk ? min(max(a.ctx_lens[(8 * j + xcd) / H], 0), (1 << 21) - 1) : 0;
-        key[j] = j < nk ? (c << kViLptBits) | (kViLptMax - 1 - j) : -1;
-      }
-      __syncthreads();
-      for (int j = threadIdx.x; j < nk; j += 64 * kViWaves) {
-        const int kj = key[j];
-        int rank = 0;
-#pragma unroll 4
-        for (int i = 0; i < nk4; i += 4) {
-          const int4 c = *reinterpret_cast<const int4*>(&key[i]);
-          rank += (c.x > kj) + (c.y > kj) + (c.z > kj) + (c.w > kj);
-        }
-        if (rank == m) s_pick = 8 * j + xcd;
-      }
-      __syncthreads();
-      unit = __builtin_amdgcn_readfirstlane(s_pick);
-    }
+    if (nk <= kLptMax)
+      unit = lpt_pick<64 * kViWaves>(reinterpret_cast<int*>(&smem[0]), &s_pick, nk, unit >> 3, xcd,
+                                     [&](int j) { return max(a.ctx_lens[(8 * j + xcd) / H], 0); });
   }
   const int b = unit / H, kvh = unit - b * H;
   const int ctx = __builtin_amdgcn_readfirstlane(max(a.ctx_lens[b], 0));
