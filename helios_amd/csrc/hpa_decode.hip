@@ -163,6 +163,15 @@ static int paged_decode(const void* q, void* out, int q_dtype, const void* k_poo
     pa.num_blocks = num_blocks;
     pa.scale_log2 = sm_scale * 1.4426950408889634f;
     pa.uniform_q = q_per_seq;
+    // The int8 verify kernel may cut long units in two; the pieces use the
+    // caller's workspace (its counter region, then piece slots), when given.
+    if (ws_kind == Ws::Caller && workspace && workspace_bytes > kCounterBytes &&
+        (long)num_seqs * num_kv_heads <= kMaxUnits) {
+      pa.counters = reinterpret_cast<int*>(workspace);
+      pa.pieces = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + kCounterBytes);
+      pa.piece_slots = (int)std::min<size_t>((workspace_bytes - kCounterBytes) / (sizeof(float) * kViSlotFloats),
+                                             (size_t)1 << 20);
+    }
     if (nt == 4 && launch_verify_i8(pa, q_dtype, kv_dtype, scale_dtype, head_dim, stream))
       return check_launch("hpa_paged_decode");
     if (launch_prefill_mfma(pa, q_dtype, kv_dtype, scale_dtype, head_dim, q_per_seq, stream))

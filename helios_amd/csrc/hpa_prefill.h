@@ -7,6 +7,10 @@
 
 namespace hpa {
 
+// A piece slot of verify_i8_kernel's split-K: one wave pair's unnormalised O
+// (64 floats per lane) and (m, l) per lane.
+constexpr int kViSlotFloats = 2 * 64 * 64 + 2 * 64 * 2;
+
 struct PrefillArgs {
   const void* q;
   void* out;
@@ -30,6 +34,16 @@ struct PrefillArgs {
   // q_pos are not read: sequence b's tokens are [b uniform_q, (b + 1)
   // uniform_q) and its first token sits at ctx_lens[b] - uniform_q.
   int uniform_q;
+  // verify_i8_kernel's split-K (read by no other kernel): one arrival
+  // counter per (sequence, KV head), zero between calls; piece_slots slots
+  // of kViSlotFloats floats for cut units' pieces (0: no unit is cut).
+  // xcd_slots: workgroups resident per XCD, which sets the length a unit
+  // must exceed to be cut.
+  int* counters = nullptr;
+  float* pieces = nullptr;
+  int piece_slots = 0;
+  int xcd_slots = 0;
+  int cut_budget = 0;  // units that may be cut per XCD (set by the launcher)
 };
 
 // Sequence b's query tokens [q0, q0 + qn), the first at position pos0, with

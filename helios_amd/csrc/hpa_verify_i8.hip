@@ -33,6 +33,7 @@
 //    32 db + 16 (g % 2) + 8 (s % 2) (layout measured on gfx950).
 // LDS rows are 16-byte chunks XOR-swizzled by (row / 2) % (chunks per row);
 // the copies apply the permutation on the global side.
+#include <algorithm>
 #include <type_traits>
 
 #include "hpa_attn_core.h"
@@ -48,6 +49,13 @@ constexpr int kViStages = 4;   // LDS stages; copies run kViStages - 1 steps ahe
 // rescale only when a row max grows by more than 2^kViLazy, so P <= 16 and
 // P * vs stays inside fp16 for every scale of an fp16-range value (vs < 517)
 constexpr int kViLazy = 4;
+
+// split-K: a unit is cut in two when its steps exceed its XCD's steps per
+// resident workgroup and kViMinPiece (piece slots: kViSlotFloats)
+constexpr int kViMinPiece = 16;
+// device-scope (sc1) buffer accesses: pieces travel between workgroups on
+// different XCDs, whose L2 caches are not coherent with each other
+constexpr int kViCoherent = 16;
 
 __host__ __device__ constexpr int vi_vmcnt(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
 
@@ -164,6 +172,7 @@ __global__ __launch_bounds__(64 * kViWaves, 2) void verify_i8_kernel(const Prefi
   static_assert((NS & (NS - 1)) == 0 && (NS - 2) * LPW < 64, "stage mask; copy waits fit vmcnt");
   __shared__ __attribute__((aligned(16))) uint8_t smem[NS * SB];
   __shared__ int s_pick;
+  __shared__ int s_red[2];
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -171,19 +180,78 @@ __global__ __launch_bounds__(64 * kViWaves, 2) void verify_i8_kernel(const Prefi
   const int units = a.num_seqs * a.num_kv_heads;
   const int T = a.uniform_q, G = a.group, H = a.num_kv_heads;
 
-  // ---- which unit this workgroup runs: longest-first per XCD
+  // ---- the work item of this workgroup: a unit, longest-first per XCD
+  // (workgroup 8 m + x, x its XCD, runs the item of rank m there).  With
+  // cutting on, the `cuts` longest units of the XCD whose n steps exceed
+  // both kViMinPiece and the XCD's steps per resident workgroup (at most
+  // a.cut_budget of them) are cut into steps [0, h) and [h, n), h =
+  // ceil(n / 2): items 2 r and 2 r + 1 are the pieces of the unit of rank r,
+  // then the other units follow longest-first.  Workgroups past the XCD's
+  // item count return at once.
   int unit = (int)blockIdx.x;
+  int s_begin = 0, s_end = -1, piece = -1, slot = 0;
   {
-    const int xcd = unit & 7;
-    const int nk = ((int)gridDim.x - xcd + 7) >> 3;
-    if (nk <= kLptMax)
-      unit = lpt_pick<64 * kViWaves>(reinterpret_cast<int*>(&smem[0]), &s_pick, nk, unit >> 3, xcd,
-                                     [&](int j) { return max(a.ctx_lens[(8 * j + xcd) / H], 0); });
+    const int xcd = unit & 7, m = unit >> 3;
+    int* lds = reinterpret_cast<int*>(&smem[0]);
+    if (a.cut_budget <= 0) {
+      const int nk = ((int)gridDim.x - xcd + 7) >> 3;
+      if (nk <= kLptMax)
+        unit = lpt_pick<64 * kViWaves>(lds, &s_pick, nk, m, xcd,
+                                       [&](int j) { return max(a.ctx_lens[(8 * j + xcd) / H], 0); });
+    } else {
+      // the launcher cuts only when nk <= kLptMax / 2
+      const int nk = (units - xcd + 7) >> 3, nk4 = (nk + 3) & ~3;
+      int* ukey = lds;                 // [kLptMax / 2] steps above inverted index
+      int* at = lds + kLptMax / 2;     // [kLptMax / 2] the unit of each rank
+      if (threadIdx.x == 0) {
+        s_red[0] = 0;
+        s_red[1] = 0;
+      }
+      __syncthreads();
+      int tot = 0;
+      for (int j = threadIdx.x; j < nk4; j += 64 * kViWaves) {
+        const int n = j < nk ? (max(a.ctx_lens[(8 * j + xcd) / H], 0) + 31) >> 5 : 0;
+        ukey[j] = j < nk ? (min(n, (1 << (30 - kLptBits)) - 1) << kLptBits) | (kLptMax - 1 - j) : -1;
+        tot += n;
+      }
+      atomicAdd(&s_red[0], tot);
+      __syncthreads();
+      const int cap = max((s_red[0] + a.xcd_slots - 1) / max(a.xcd_slots, 1), kViMinPiece);
+      int over = 0;
+      for (int j = threadIdx.x; j < nk; j += 64 * kViWaves) over += (ukey[j] >> kLptBits) > cap;
+      atomicAdd(&s_red[1], over);
+      __syncthreads();
+      const int cuts = min(s_red[1], a.cut_budget);  // the units of ranks [0, cuts)
+      if (m >= nk + cuts) return;                    // no item for this workgroup
+      for (int j = threadIdx.x; j < nk; j += 64 * kViWaves) {
+        const int kj = ukey[j];
+        int rank = 0;
+#pragma unroll 4
+        for (int i = 0; i < nk4; i += 4) {
+          const int4 c = *reinterpret_cast<const int4*>(&ukey[i]);
+          rank += (c.x > kj) + (c.y > kj) + (c.z > kj) + (c.w > kj);
+        }
+        at[rank] = j;
+      }
+      __syncthreads();
+      const int rk = m < 2 * cuts ? m >> 1 : m - cuts;
+      const int j = __builtin_amdgcn_readfirstlane(at[rk]);
+      unit = 8 * j + xcd;
+      if (m < 2 * cuts) {
+        const int n = __builtin_amdgcn_readfirstlane(ukey[j] >> kLptBits);
+        piece = m & 1;
+        s_begin = piece ? (n + 1) >> 1 : 0;
+        s_end = piece ? n : (n + 1) >> 1;
+        slot = 2 * (8 * rk + xcd);
+      }
+      __syncthreads();  // every thread has read its item before the copies reuse the LDS
+    }
   }
   const int b = unit / H, kvh = unit - b * H;
   const int ctx = __builtin_amdgcn_readfirstlane(max(a.ctx_lens[b], 0));
   const int rows = T * G;
   const int nsteps = (ctx + 31) >> 5;
+  if (piece < 0) s_end = nsteps;
   const int q0 = b * T, pos0 = ctx - T;
 
   // ---- this lane's row and its query fragments: MFMA c takes dims
@@ -238,7 +306,7 @@ __global__ __launch_bounds__(64 * kViWaves, 2) void verify_i8_kernel(const Prefi
     for (int hf = 0; hf < 2; ++hf) {
       const int key0 = 32 * step + 16 * hf;
       const int left = ctx - key0;
-      int valid = step >= nsteps ? 0 : left >= 16 ? 16 : left > 0 ? left : 0;
+      int valid = step >= s_end ? 0 : left >= 16 ? 16 : left > 0 ? left : 0;
       int phys = 0;
       if (valid > 0) {
         const int lb = key0 >> a.bs_log2;
@@ -416,15 +484,87 @@ __global__ __launch_bounds__(64 * kViWaves, 2) void verify_i8_kernel(const Prefi
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_waitcnt(0x0F70);
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  for (int u = 0; u < NS - 1; ++u) issue_copy(u);
-  for (int i = 0; i < nsteps; ++i) step(i);
+  for (int u = 0; u < NS - 1; ++u) issue_copy(s_begin + u);
+  for (int i = s_begin; i < s_end; ++i) step(i);
   // the empty copies issued past the last step still write LDS
   __builtin_amdgcn_s_waitcnt(0x0F70);
 
   // ---- epilogue: O = (O'^T - 1152 sum(P')) / l; o[db][v] is dim
   // 32 db + 8 (v / 4) + 4 h + v % 4 of row n
   const float lt = vi_pair_sum(l), ot = 1152.f * vi_pair_sum(loff);
-  const float inv = lt > 0.f ? 1.f / lt : 0.f;
+#pragma unroll
+  for (int db = 0; db < DB; ++db) o[db] = o[db] - ot;  // unnormalised O
+  float inv = lt > 0.f ? 1.f / lt : 0.f;
+  if (piece >= 0) {
+    // A cut unit.  The piece that finishes second merges both (in piece
+    // order, so the result does not depend on which one that is) and
+    // returns the unit's counter to zero; the first publishes its (O, m, l)
+    // and leaves.  A piece that finds the other already counted merges
+    // without publishing.
+    const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(a.pieces, (short)0, 0x7fffffff, 0x00020000);
+    const int li = 64 * w + lane;
+    const uint32_t own = (uint32_t)((slot + piece) * kViSlotFloats) * 4u;
+    const uint32_t oth = (uint32_t)((slot + 1 - piece) * kViSlotFloats) * 4u;
+    const uint32_t uo = (uint32_t)li * 256u, mlo = (uint32_t)(2 * 64 * 64 + 2 * li) * 4u;
+    int* ctr = a.counters + unit;
+    if (threadIdx.x == 0) s_red[0] = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    bool merge = s_red[0] == 1;
+    __syncthreads();
+    if (!merge) {
+      // (elements are copied out before the bit casts: a bit_cast applied
+      // directly to an ext_vector element reads element 0 with hipcc 7.2)
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const float e0 = o[db][4 * c], e1 = o[db][4 * c + 1], e2 = o[db][4 * c + 2], e3 = o[db][4 * c + 3];
+          __builtin_amdgcn_raw_buffer_store_b128(
+              (u32x4){__builtin_bit_cast(uint32_t, e0), __builtin_bit_cast(uint32_t, e1),
+                      __builtin_bit_cast(uint32_t, e2), __builtin_bit_cast(uint32_t, e3)},
+              pr, own + uo + 64 * db + 16 * c, 0, kViCoherent);
+        }
+      __builtin_amdgcn_raw_buffer_store_b64((u32x2){__builtin_bit_cast(uint32_t, m), __builtin_bit_cast(uint32_t, lt)},
+                                            pr, own + mlo, 0, kViCoherent);
+      // counted once both waves' stores are complete (hence visible device-wide)
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      __builtin_amdgcn_s_waitcnt(0);
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      __syncthreads();
+      if (threadIdx.x == 0) s_red[1] = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __syncthreads();
+      merge = s_red[1] == 1;
+    }
+    if (!merge) return;
+    if (threadIdx.x == 0) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    f32x16v uo2[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(pr, oth + uo + 64 * db + 16 * c, 0, kViCoherent);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t xe = x[e];
+          uo2[db][4 * c + e] = __builtin_bit_cast(float, xe);
+        }
+      }
+    const u32x2 mlx = __builtin_amdgcn_raw_buffer_load_b64(pr, oth + mlo, 0, kViCoherent);
+    const uint32_t mlx0 = mlx[0], mlx1 = mlx[1];
+    const float mo = __builtin_bit_cast(float, mlx0), lo2 = __builtin_bit_cast(float, mlx1);
+    const float m0 = piece == 0 ? m : mo, m1 = piece == 0 ? mo : m;
+    const float l0 = piece == 0 ? lt : lo2, l1 = piece == 0 ? lo2 : lt;
+    const float mm = fmaxf(m0, m1);
+    const float a0 = mm == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m0 - mm);
+    const float a1 = mm == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - mm);
+    const float ll = l0 * a0 + l1 * a1;
+    inv = ll > 0.f ? 1.f / ll : 0.f;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      const f32x16v u0 = piece == 0 ? o[db] : uo2[db], u1 = piece == 0 ? uo2[db] : o[db];
+      o[db] = u0 * a0 + u1 * a1;
+    }
+  }
   if (rv) {
     uint16_t* orow = reinterpret_cast<uint16_t*>(a.out) + ((long)(q0 + t) * a.num_q_heads + kvh * G + hh) * D + 4 * h;
 #pragma unroll
@@ -432,13 +572,47 @@ __global__ __launch_bounds__(64 * kViWaves, 2) void verify_i8_kernel(const Prefi
 #pragma unroll
       for (int v4 = 0; v4 < 4; ++v4) {
         u32x2 pk;
-        pk[0] = __builtin_bit_cast(uint32_t, (f16x2){(_Float16)((o[db][4 * v4] - ot) * inv),
-                                                     (_Float16)((o[db][4 * v4 + 1] - ot) * inv)});
-        pk[1] = __builtin_bit_cast(uint32_t, (f16x2){(_Float16)((o[db][4 * v4 + 2] - ot) * inv),
-                                                     (_Float16)((o[db][4 * v4 + 3] - ot) * inv)});
+        pk[0] = __builtin_bit_cast(uint32_t, (f16x2){(_Float16)(o[db][4 * v4] * inv), (_Float16)(o[db][4 * v4 + 1] * inv)});
+        pk[1] = __builtin_bit_cast(uint32_t,
+                                   (f16x2){(_Float16)(o[db][4 * v4 + 2] * inv), (_Float16)(o[db][4 * v4 + 3] * inv)});
         *reinterpret_cast<u32x2*>(orow + 32 * db + 8 * v4) = pk;
       }
   }
+}
+
+template <class ST, int D>
+static void vi_launch(PrefillArgs a, long units, hipStream_t s) {
+  static int per_cu = 0;  // workgroups resident per CU
+  if (!per_cu) {
+    int nb = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void*>(&verify_i8_kernel<ST, D>),
+                                                     64 * kViWaves, 0) != hipSuccess || nb <= 0)
+      nb = 1;
+    per_cu = nb;
+  }
+  static int cus_of[64];
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64) {
+    if (!cus_of[dev] && (hipDeviceGetAttribute(&cus_of[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+                         cus_of[dev] <= 0))
+      cus_of[dev] = 256;
+    cus = cus_of[dev];
+  }
+  // Cutting needs the workspace (two piece slots per cut unit, 8 XCDs) and
+  // at most kLptMax / 2 units per XCD.  Per XCD it may cut up to a quarter of
+  // its units, or as many as leave resident workgroups idle otherwise.
+  const long nk = (units + 7) / 8;
+  const int xcd_slots = std::max(1, cus * per_cu / 8);
+  const long slots = std::min<long>(a.piece_slots, 0x7fffffffL / (4L * kViSlotFloats));
+  long budget = std::max<long>(nk / 4, std::min<long>(nk, xcd_slots - nk));
+  budget = std::min<long>(budget, slots / 16);
+  const bool cut = a.counters && a.pieces && nk <= kLptMax / 2 && budget > 0;
+  a.cut_budget = cut ? (int)budget : 0;
+  a.xcd_slots = xcd_slots;
+  // cutting: every XCD gets nk + budget workgroups, enough for both pieces of
+  // every cut unit on the XCD with the most units
+  const dim3 grid((unsigned)(cut ? 8 * (nk + budget) : units)), block(64 * kViWaves);
+  hipLaunchKernelGGL((verify_i8_kernel<ST, D>), grid, block, 0, s, a);
 }
 
 bool launch_verify_i8(const PrefillArgs& a, int q_dtype, int kv_dtype, int scale_dtype, int head_dim,
@@ -448,14 +622,13 @@ bool launch_verify_i8(const PrefillArgs& a, int q_dtype, int kv_dtype, int scale
   const long rows = (long)a.uniform_q * a.group;
   if (rows <= 32 || rows > 32 * kViWaves) return false;
   const long units = (long)a.num_seqs * a.num_kv_heads;
-  if (units <= 0 || units > 0x7fffffffL) return false;
-  const dim3 grid((unsigned)units), block(64 * kViWaves);
+  if (units <= 0 || units > 0x3fffffffL) return false;
   if (scale_dtype == HPA_F16) {
-    if (head_dim == 128) hipLaunchKernelGGL((verify_i8_kernel<F16, 128>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((verify_i8_kernel<F16, 64>), grid, block, 0, s, a);
+    if (head_dim == 128) vi_launch<F16, 128>(a, units, s);
+    else vi_launch<F16, 64>(a, units, s);
   } else if (scale_dtype == HPA_F32) {
-    if (head_dim == 128) hipLaunchKernelGGL((verify_i8_kernel<F32, 128>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((verify_i8_kernel<F32, 64>), grid, block, 0, s, a);
+    if (head_dim == 128) vi_launch<F32, 128>(a, units, s);
+    else vi_launch<F32, 64>(a, units, s);
   } else {
     return false;
   }

@@ -274,6 +274,26 @@ def test_int8_wide_verify_dequantises_in_registers(Hq, Hkv, T, D, scale_dtype):
     assert torch.equal(got, again)
 
 
+def test_int8_wide_verify_cuts_long_units():
+    """A few long contexts: the verify kernel cuts units longer than their
+    XCD's steps per resident workgroup in two, and the piece that finishes
+    second merges both in piece order.  The result matches the oracle, two
+    calls give the same bits, and the arrival counters are back at zero
+    afterwards: a decode on the same workspace, whose own split-K counts on
+    them, still matches the oracle."""
+    print("int8 verify, cut units", flush=True)
+    T = 12
+    lens = [T, 900, 4000, 7003, 2500]
+    cache, tables, q = _case(160, len(lens), lens, 32, 8, 128, 16, torch.float16, quant=True, q_per_seq=T)
+    got = paged_attention_verify_batched(q, cache, tables, lens, T)
+    _check(got, _oracle_decode(cache, q, tables, lens, q_per_seq=T), torch.float16, "cut units")
+    again = paged_attention_verify_batched(q, cache, tables, lens, T)
+    assert torch.equal(got, again)
+    qd = q[T - 1::T].contiguous()
+    dec = paged_attention_decode_batched(qd, cache, tables, lens)
+    _check(dec, _oracle_decode(cache, qd, tables, lens), torch.float16, "decode after cut verify")
+
+
 def test_int8_wide_verify_many_sequences_and_scale_range():
     """Config 5's head shape with 12 speculative tokens (48 rows per KV
     head) over 300 sequences, so workgroups run longest-first over several
