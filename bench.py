@@ -647,6 +647,87 @@ def spec_bench(device, gamma, steps, warmup, seed=4):
     }))
 
 
+def helios_shape_bench(device, steps, warmup):
+    """helios' only published measurement of this path
+    (tests/parity/test_triton_parity.py:125-175; numbers in
+    exec/triton_attn.py:3-7): fp16 paged decode of 32 sequences x 512
+    context, Hq 32 / Hkv 8, head_dim 128, block 16, sequence i on blocks
+    [32 i, 32 i + 32), pool and queries drawn after torch.manual_seed(3).
+    Timed two ways:
+    - the kernel alone: median over chunks of 10 calls between HIP event
+      pairs, with int32 device tables and lengths;
+    - helios' own protocol: wall clock over 20 calls after 5 warmups,
+      synchronised before and after, through paged_attention_decode_hip with
+      Python lists (converted per call, as helios' wrapper does).
+    helios measured 2.676 ms (Triton) and 14.089 ms (PyTorch path) on a
+    Tesla T4; that is other hardware, so no ratio is reported as a
+    baseline.  The 67 MB pool fits in the 256 MB Infinity Cache and, as in
+    helios' protocol, every call reads the same pool, so repeated calls are
+    served largely from that cache rather than HBM."""
+    import torch
+
+    import helios_amd as H
+
+    torch.manual_seed(3)
+    bs, hkv, hq, d, n, ctx = 16, 8, 32, 128, 32, 512
+    need = ctx // bs
+    cache = H.PagedKVCache(n * need + 8, bs, hkv, d, dtype=torch.float16, device=device)
+    cache.k_cache.normal_()
+    cache.v_cache.normal_()
+    tables = [[i * need + j for j in range(need)] for i in range(n)]
+    lens = [ctx] * n
+    q = torch.randn(n, hq, d, dtype=torch.float16, device=device)
+    tt = torch.tensor(tables, dtype=torch.int32, device=device)
+    lt = torch.tensor(lens, dtype=torch.int32, device=device)
+    out = torch.empty_like(q)
+    ws = H.decode_workspace(n, 1, hq, hkv, d, ctx, device=device)
+
+    def call():
+        H.paged_attention_decode_hip(q, cache.k_cache, cache.v_cache, tt, lt, max_context_len=ctx, out=out,
+                                     workspace=ws)
+
+    stream = torch.cuda.current_stream(device)
+    for _ in range(max(warmup, 5)):
+        call()
+    torch.cuda.synchronize()
+    chunks = max(1, steps // 10)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(chunks)]
+    for a, b in ev:
+        a.record(stream)
+        for _ in range(10):
+            call()
+        b.record(stream)
+    torch.cuda.synchronize()
+    ms = sorted(a.elapsed_time(b) / 10 for a, b in ev)
+    kernel_ms = ms[len(ms) // 2]
+
+    def helios_protocol():
+        return H.paged_attention_decode_hip(q, cache.k_cache, cache.v_cache, tables, lens)
+
+    for _ in range(5):
+        helios_protocol()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(20):
+        helios_protocol()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / 20
+    kv_bytes = n * ctx * 2 * hkv * d * 2
+    print(json.dumps({
+        "metric": "paged decode at helios' published shape (32 seqs x 512 ctx, Hq 32 / Hkv 8, D 128, fp16, "
+                  "block 16)",
+        "value": round(kernel_ms, 4), "unit": "ms per call", "higher_is_better": False,
+        "kernel_ms": round(kernel_ms, 4),
+        "helios_protocol_wall_ms": round(wall_ms, 4),
+        "kv_gbs_kernel": round(kv_bytes / (kernel_ms * 1e-3) / 1e9, 1),
+        "kv_bytes": kv_bytes,
+        "reference_published": {"hardware": "Tesla T4", "triton_ms": 2.676, "pytorch_ms": 14.089,
+                                "source": "exec/triton_attn.py:3-7"},
+        "vs_baseline": None,
+        "dtype": "f16", "data": "synthetic (torch.manual_seed(3), N(0,1) pool and queries)",
+    }))
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -675,6 +756,8 @@ def main():
     ap.add_argument("--spec-gamma", type=int, default=0, metavar="G",
                     help="only time one speculative step's attention (gamma G, config 5 batch) "
                          "batched vs per sequence, print its own JSON line, and exit")
+    ap.add_argument("--helios-shape", action="store_true",
+                    help="time the decode at helios' only published shape (32 seqs x 512 ctx, fp16) instead")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run 5 plain device copies of MIB MiB (the known-size kernel "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings) and exit")
@@ -711,6 +794,9 @@ def main():
         return
     if args.spec_gamma:
         spec_bench(device, args.spec_gamma, min(args.steps, 50), min(args.warmup, 20))
+        return
+    if args.helios_shape:
+        helios_shape_bench(device, args.steps, args.warmup)
         return
     if args.meta_layers:
         meta_bench(device, args.meta_layers, min(args.steps, 20), min(args.warmup, 5))
