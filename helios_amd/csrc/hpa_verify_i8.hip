@@ -53,6 +53,7 @@ constexpr int kViLazy = 4;
 // split-K: a unit is cut in two when its steps exceed its XCD's steps per
 // resident workgroup and kViMinPiece (piece slots: kViSlotFloats)
 constexpr int kViMinPiece = 16;
+constexpr int kViMaxPieces = 4;  // pieces per cut unit
 // device-scope (sc1) buffer accesses: pieces travel between workgroups on
 // different XCDs, whose L2 caches are not coherent with each other
 constexpr int kViCoherent = 16;
@@ -184,12 +185,13 @@ __global__ __launch_bounds__(64 * kViWaves, 2) void verify_i8_kernel(const Prefi
   // (workgroup 8 m + x, x its XCD, runs the item of rank m there).  With
   // cutting on, the `cuts` longest units of the XCD whose n steps exceed
   // both kViMinPiece and the XCD's steps per resident workgroup (at most
-  // a.cut_budget of them) are cut into steps [0, h) and [h, n), h =
-  // ceil(n / 2): items 2 r and 2 r + 1 are the pieces of the unit of rank r,
-  // then the other units follow longest-first.  Workgroups past the XCD's
-  // item count return at once.
+  // a.cut_budget of them) are cut into P pieces of steps [p n / P, (p + 1)
+  // n / P): P = 2, or up to kViMaxPieces when that still leaves no item
+  // waiting for a resident workgroup.  Items P r .. P r + P - 1 are the
+  // pieces of the unit of rank r, then the other units follow
+  // longest-first.  Workgroups past the XCD's item count return at once.
   int unit = (int)blockIdx.x;
-  int s_begin = 0, s_end = -1, piece = -1, slot = 0;
+  int s_begin = 0, s_end = -1, piece = -1, pieces = 0, slot = 0;
   {
     const int xcd = unit & 7, m = unit >> 3;
     int* lds = reinterpret_cast<int*>(&smem[0]);
@@ -221,8 +223,11 @@ __global__ __launch_bounds__(64 * kViWaves, 2) void verify_i8_kernel(const Prefi
       for (int j = threadIdx.x; j < nk; j += 64 * kViWaves) over += (ukey[j] >> kLptBits) > cap;
       atomicAdd(&s_red[1], over);
       __syncthreads();
-      const int cuts = min(s_red[1], a.cut_budget);  // the units of ranks [0, cuts)
-      if (m >= nk + cuts) return;                    // no item for this workgroup
+      // (read through readfirstlane: values from LDS count as divergent, and
+      // a divergent step range would put every copy's descriptor in a loop)
+      const int cuts = __builtin_amdgcn_readfirstlane(min(s_red[1], a.cut_budget));  // ranks [0, cuts)
+      const int np = cuts > 0 ? min(max((a.xcd_slots - nk + cuts) / cuts, 2), kViMaxPieces) : 2;
+      if (m >= nk + (np - 1) * cuts) return;  // no item for this workgroup
       for (int j = threadIdx.x; j < nk; j += 64 * kViWaves) {
         const int kj = ukey[j];
         int rank = 0;
@@ -234,15 +239,18 @@ __global__ __launch_bounds__(64 * kViWaves, 2) void verify_i8_kernel(const Prefi
         at[rank] = j;
       }
       __syncthreads();
-      const int rk = m < 2 * cuts ? m >> 1 : m - cuts;
+      const int rk = __builtin_amdgcn_readfirstlane(m < np * cuts ? m / np : m - (np - 1) * cuts);
       const int j = __builtin_amdgcn_readfirstlane(at[rk]);
       unit = 8 * j + xcd;
-      if (m < 2 * cuts) {
+      if (m < np * cuts) {
         const int n = __builtin_amdgcn_readfirstlane(ukey[j] >> kLptBits);
-        piece = m & 1;
-        s_begin = piece ? (n + 1) >> 1 : 0;
-        s_end = piece ? n : (n + 1) >> 1;
-        slot = 2 * (8 * rk + xcd);
+        piece = m - np * rk;
+        pieces = np;
+        // (the divisions by np run on the vector unit; readfirstlane keeps the
+        // step range, and with it every copy's descriptor, in scalar registers)
+        s_begin = __builtin_amdgcn_readfirstlane(piece * n / np);
+        s_end = __builtin_amdgcn_readfirstlane((piece + 1) * n / np);
+        slot = kViMaxPieces * (8 * rk + xcd);
       }
       __syncthreads();  // every thread has read its item before the copies reuse the LDS
     }
@@ -496,22 +504,22 @@ __global__ __launch_bounds__(64 * kViWaves, 2) void verify_i8_kernel(const Prefi
   for (int db = 0; db < DB; ++db) o[db] = o[db] - ot;  // unnormalised O
   float inv = lt > 0.f ? 1.f / lt : 0.f;
   if (piece >= 0) {
-    // A cut unit.  The piece that finishes second merges both (in piece
+    // A cut unit.  The piece that arrives last merges all of them (in piece
     // order, so the result does not depend on which one that is) and
-    // returns the unit's counter to zero; the first publishes its (O, m, l)
-    // and leaves.  A piece that finds the other already counted merges
+    // returns the unit's counter to zero; the others publish their (O, m,
+    // l) and leave.  A piece that finds the others already counted merges
     // without publishing.
     const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(a.pieces, (short)0, 0x7fffffff, 0x00020000);
     const int li = 64 * w + lane;
-    const uint32_t own = (uint32_t)((slot + piece) * kViSlotFloats) * 4u;
-    const uint32_t oth = (uint32_t)((slot + 1 - piece) * kViSlotFloats) * 4u;
     const uint32_t uo = (uint32_t)li * 256u, mlo = (uint32_t)(2 * 64 * 64 + 2 * li) * 4u;
+    auto slot_off = [&](int p) { return (uint32_t)((slot + p) * kViSlotFloats) * 4u; };
     int* ctr = a.counters + unit;
     if (threadIdx.x == 0) s_red[0] = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
-    bool merge = s_red[0] == 1;
+    bool merge = s_red[0] == pieces - 1;
     __syncthreads();
     if (!merge) {
+      const uint32_t own = slot_off(piece);
       // (elements are copied out before the bit casts: a bit_cast applied
       // directly to an ext_vector element reads element 0 with hipcc 7.2)
 #pragma unroll
@@ -533,37 +541,66 @@ __global__ __launch_bounds__(64 * kViWaves, 2) void verify_i8_kernel(const Prefi
       __syncthreads();
       if (threadIdx.x == 0) s_red[1] = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __syncthreads();
-      merge = s_red[1] == 1;
+      merge = s_red[1] == pieces - 1;
     }
     if (!merge) return;
     if (threadIdx.x == 0) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    f32x16v uo2[DB];
+    // every piece's (m, l): this one's from registers, the others' from
+    // their slots; then the pieces' O in piece order, rescaled to the
+    // largest m
+    float mp[kViMaxPieces], lp[kViMaxPieces];
+    float mm = -INFINITY;
 #pragma unroll
-    for (int db = 0; db < DB; ++db)
+    for (int p = 0; p < kViMaxPieces; ++p) {
+      mp[p] = -INFINITY;
+      lp[p] = 0.f;
+      if (p < pieces) {
+        if (p == piece) {
+          mp[p] = m;
+          lp[p] = lt;
+        } else {
+          const u32x2 mlx = __builtin_amdgcn_raw_buffer_load_b64(pr, slot_off(p) + mlo, 0, kViCoherent);
+          const uint32_t mlx0 = mlx[0], mlx1 = mlx[1];
+          mp[p] = __builtin_bit_cast(float, mlx0);
+          lp[p] = __builtin_bit_cast(float, mlx1);
+        }
+        mm = fmaxf(mm, mp[p]);
+      }
+    }
+    f32x16v acc[DB];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(pr, oth + uo + 64 * db + 16 * c, 0, kViCoherent);
+    for (int db = 0; db < DB; ++db) acc[db] = (f32x16v){};
+    float ll = 0.f;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint32_t xe = x[e];
-          uo2[db][4 * c + e] = __builtin_bit_cast(float, xe);
+    for (int p = 0; p < kViMaxPieces; ++p) {
+      if (p < pieces) {
+        const float ap = mm == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mp[p] - mm);
+        ll += lp[p] * ap;
+        if (p == piece) {
+#pragma unroll
+          for (int db = 0; db < DB; ++db) acc[db] += o[db] * ap;
+        } else {
+#pragma unroll
+          for (int db = 0; db < DB; ++db) {
+            f32x16v u;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+              const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(pr, slot_off(p) + uo + 64 * db + 16 * c, 0,
+                                                                    kViCoherent);
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const uint32_t xe = x[e];
+                u[4 * c + e] = __builtin_bit_cast(float, xe);
+              }
+            }
+            acc[db] += u * ap;
+          }
         }
       }
-    const u32x2 mlx = __builtin_amdgcn_raw_buffer_load_b64(pr, oth + mlo, 0, kViCoherent);
-    const uint32_t mlx0 = mlx[0], mlx1 = mlx[1];
-    const float mo = __builtin_bit_cast(float, mlx0), lo2 = __builtin_bit_cast(float, mlx1);
-    const float m0 = piece == 0 ? m : mo, m1 = piece == 0 ? mo : m;
-    const float l0 = piece == 0 ? lt : lo2, l1 = piece == 0 ? lo2 : lt;
-    const float mm = fmaxf(m0, m1);
-    const float a0 = mm == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m0 - mm);
-    const float a1 = mm == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - mm);
-    const float ll = l0 * a0 + l1 * a1;
+    }
     inv = ll > 0.f ? 1.f / ll : 0.f;
 #pragma unroll
-    for (int db = 0; db < DB; ++db) {
-      const f32x16v u0 = piece == 0 ? o[db] : uo2[db], u1 = piece == 0 ? uo2[db] : o[db];
-      o[db] = u0 * a0 + u1 * a1;
-    }
+    for (int db = 0; db < DB; ++db) o[db] = acc[db];
   }
   if (rv) {
     uint16_t* orow = reinterpret_cast<uint16_t*>(a.out) + ((long)(q0 + t) * a.num_q_heads + kvh * G + hh) * D + 4 * h;
@@ -605,13 +642,13 @@ static void vi_launch(PrefillArgs a, long units, hipStream_t s) {
   const int xcd_slots = std::max(1, cus * per_cu / 8);
   const long slots = std::min<long>(a.piece_slots, 0x7fffffffL / (4L * kViSlotFloats));
   long budget = std::max<long>(nk / 4, std::min<long>(nk, xcd_slots - nk));
-  budget = std::min<long>(budget, slots / 16);
+  budget = std::min<long>(budget, slots / (8L * kViMaxPieces));
   const bool cut = a.counters && a.pieces && nk <= kLptMax / 2 && budget > 0;
   a.cut_budget = cut ? (int)budget : 0;
   a.xcd_slots = xcd_slots;
-  // cutting: every XCD gets nk + budget workgroups, enough for both pieces of
-  // every cut unit on the XCD with the most units
-  const dim3 grid((unsigned)(cut ? 8 * (nk + budget) : units)), block(64 * kViWaves);
+  // cutting: every XCD gets enough workgroups for every item: nk + budget
+  // with two pieces per cut unit, at most xcd_slots with more
+  const dim3 grid((unsigned)(cut ? 8 * std::max<long>(nk + budget, xcd_slots) : units)), block(64 * kViWaves);
   hipLaunchKernelGGL((verify_i8_kernel<ST, D>), grid, block, 0, s, a);
 }
 
