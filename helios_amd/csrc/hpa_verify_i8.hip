@@ -321,6 +321,10 @@ __global__ __launch_bounds__(64 * kViWaves, 2) void verify_i8_kernel(const Prefi
         phys = lb < a.table_stride ? ((const __attribute__((address_space(4))) int32_t*)trow)[lb] : -1;
         if ((unsigned)phys >= (unsigned)a.num_blocks) { phys = 0; valid = 0; }
       }
+      // uniform by construction; said so, because a descriptor the compiler
+      // thinks divergent is issued in a readfirstlane loop
+      valid = __builtin_amdgcn_readfirstlane(valid);
+      phys = __builtin_amdgcn_readfirstlane(phys);
       const long row0 = (long)phys * blk_rows + head_rows + (key0 & bsm);
       const __amdgpu_buffer_rsrc_t rs =
           __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(pool + row0 * D), (short)0, valid * D, 0x00020000);
