@@ -132,16 +132,20 @@ static int paged_decode(const void* q, void* out, int q_dtype, const void* k_poo
   const int group = num_q_heads / num_kv_heads;
   const int rows = group * q_per_seq;
   const int nt = decode_nt(rows);
-  if (nt == 0 || nt == 4) {
-    // More than 32 query rows per KV head (a wide speculative verify): the
-    // decode kernel's four row tiles spill registers and it takes at most
-    // 64 rows, while the prefill kernels tile any number of rows.  The MFMA
-    // prefill kernel (fp16 / bf16 queries, head_dim 64 / 128, block_size >=
-    // 16) runs these verifies several times faster; past 64 rows, shapes it
-    // does not take run on the generic prefill kernel.  Both compute the same
-    // causal rule as hpa_paged_prefill over the same tokens, in a mode where
-    // sequence b's tokens are [b q_per_seq, (b + 1) q_per_seq) and end at its
-    // context; no workspace is used.
+  if (nt != 1) {
+    // More than 16 query rows per KV head (a wide speculative verify).  With
+    // fp16 queries over an int8 pool, 17-64 rows run on the verify kernel
+    // that dequantises in registers (the decode kernel's two and four row
+    // tiles spill registers).  Otherwise, above 32 rows: the decode kernel's
+    // four row tiles spill and it takes at most 64 rows, while the prefill
+    // kernels tile any number of rows.  The MFMA prefill kernel (fp16 / bf16
+    // queries, head_dim 64 / 128, block_size >= 16) runs these verifies
+    // several times faster; past 64 rows, shapes it does not take run on the
+    // generic prefill kernel.  Both compute the same causal rule as
+    // hpa_paged_prefill over the same tokens, in a mode where sequence b's
+    // tokens are [b q_per_seq, (b + 1) q_per_seq) and end at its context; no
+    // workspace is used.  17-32 rows that the verify kernel does not take
+    // stay on the decode kernel.
     PrefillArgs pa;
     pa.q = q;
     pa.out = out;
@@ -172,9 +176,9 @@ static int paged_decode(const void* q, void* out, int q_dtype, const void* k_poo
       pa.piece_slots = (int)std::min<size_t>((workspace_bytes - kCounterBytes) / (sizeof(float) * kViSlotFloats),
                                              (size_t)1 << 20);
     }
-    if (nt == 4 && launch_verify_i8(pa, q_dtype, kv_dtype, scale_dtype, head_dim, stream))
+    if (nt != 0 && launch_verify_i8(pa, q_dtype, kv_dtype, scale_dtype, head_dim, stream))
       return check_launch("hpa_paged_decode");
-    if (launch_prefill_mfma(pa, q_dtype, kv_dtype, scale_dtype, head_dim, q_per_seq, stream))
+    if (nt != 2 && launch_prefill_mfma(pa, q_dtype, kv_dtype, scale_dtype, head_dim, q_per_seq, stream))
       return check_launch("hpa_paged_decode");
     if (nt == 0) {
       const int st = launch_prefill_generic(pa, q_dtype, kv_dtype, scale_dtype, head_dim, q_per_seq, stream);

@@ -1,4 +1,4 @@
-// Wide speculative verify over int8 pools: 33-64 query rows per KV head
+// Wide speculative verify over int8 pools: 17-64 query rows per KV head
 // (helios' verify prefill, exec/runner.py:354-362, batched over sequences),
 // fp16 queries, head_dim 64 or 128, block_size >= 16.
 //
@@ -265,6 +265,7 @@ __global__ __launch_bounds__(64 * kViWaves, 2) void verify_i8_kernel(const Prefi
   // ---- this lane's row and its query fragments: MFMA c takes dims
   // [16 c + 8 h, + 8); the row's sum of q enters the offset term
   const int r = 32 * w + n;
+  const bool busy = 32 * w < rows;  // wave-uniform: this wave holds rows
   const bool rv = r < rows && q0 + r / G < a.num_tokens;
   const int t = r / G, hh = r - t * G;
   const int lim = rv ? max(min(pos0 + t + 1, ctx), 0) : 0;
@@ -381,6 +382,7 @@ __global__ __launch_bounds__(64 * kViWaves, 2) void verify_i8_kernel(const Prefi
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     // every wave has read step i - 1's stage, which step i + NS - 1 refills
     issue_copy(i + NS - 1);
+    if (!busy) return;  // a wave without rows only copies
     const uint32_t sl = vi_lds_addr(&smem[(i & (NS - 1)) * SB]);
     // ---- LDS reads, in this order: the K operand bytes, the scales of the
     // lane's 16 keys (runs 16 kc + 8 h + [0, 8), K then V), the V^T bytes
@@ -661,7 +663,7 @@ bool launch_verify_i8(const PrefillArgs& a, int q_dtype, int kv_dtype, int scale
   if (q_dtype != HPA_F16 || kv_dtype != HPA_I8 || !a.ks || !a.vs || a.uniform_q <= 0) return false;
   if (a.bs_log2 < 4 || (head_dim != 64 && head_dim != 128)) return false;
   const long rows = (long)a.uniform_q * a.group;
-  if (rows <= 32 || rows > 32 * kViWaves) return false;
+  if (rows <= 16 || rows > 32 * kViWaves) return false;
   const long units = (long)a.num_seqs * a.num_kv_heads;
   if (units <= 0 || units > 0x3fffffffL) return false;
   if (scale_dtype == HPA_F16) {

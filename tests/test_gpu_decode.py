@@ -254,9 +254,10 @@ def test_wide_verify_runs_the_mfma_prefill_kernel(Hq, Hkv, T, D, dtype, quant):
 
 @pytest.mark.parametrize("scale_dtype", [torch.float16, torch.float32])
 @pytest.mark.parametrize("Hq,Hkv,T,D", [(8, 1, 5, 128), (32, 4, 8, 128), (14, 2, 5, 64), (16, 2, 7, 64),
-                                        (32, 8, 16, 128)])
+                                        (32, 8, 16, 128), (8, 1, 3, 128), (14, 2, 3, 64), (32, 8, 8, 128)])
 def test_int8_wide_verify_dequantises_in_registers(Hq, Hkv, T, D, scale_dtype):
-    """33-64 rows per KV head, fp16 queries over an int8 pool: the verify
+    """33-64 rows per KV head (17-32 in test_verify_rows_and_gqa_groups),
+    fp16 queries over an int8 pool: the verify
     kernel that turns each wave's own int8 operands into fp16 in registers
     (1152 + x, offsets removed algebraically) against the oracle on the
     exactly dequantised values.  Contexts cover a context equal to the token
