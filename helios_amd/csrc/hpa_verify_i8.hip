@@ -19,7 +19,10 @@
 // 2^-22, so no per-key rounding of the weights reaches the output.  No
 // dequantised tile is written back to LDS and no step waits for one.
 // A workgroup then needs only the int8 stages (33 KB at head_dim 128), four
-// workgroups share a CU, and every wave holds rows.
+// workgroups share a CU, and every wave holds rows (with 17-32 rows the
+// second wave only copies).  With a workspace, the longest units of an XCD
+// are cut into 2-4 pieces that run on separate workgroups; the last piece to
+// finish merges them in piece order.
 //
 // Operand layouts (lane l, h = l / 32, n = l % 32):
 //  - S^T's A operand row m is key pi(m) (bits 2 and 3 of m swapped), so the
@@ -50,8 +53,8 @@ constexpr int kViStages = 4;   // LDS stages; copies run kViStages - 1 steps ahe
 // P * vs stays inside fp16 for every scale of an fp16-range value (vs < 517)
 constexpr int kViLazy = 4;
 
-// split-K: a unit is cut in two when its steps exceed its XCD's steps per
-// resident workgroup and kViMinPiece (piece slots: kViSlotFloats)
+// split-K: a unit is cut when its steps exceed its XCD's steps per resident
+// workgroup and kViMinPiece (piece slots: kViSlotFloats)
 constexpr int kViMinPiece = 16;
 constexpr int kViMaxPieces = 4;  // pieces per cut unit
 // device-scope (sc1) buffer accesses: pieces travel between workgroups on
