@@ -144,8 +144,10 @@ static int paged_decode(const void* q, void* out, int q_dtype, const void* k_poo
     // generic prefill kernel.  Both compute the same causal rule as
     // hpa_paged_prefill over the same tokens, in a mode where sequence b's
     // tokens are [b q_per_seq, (b + 1) q_per_seq) and end at its context; no
-    // workspace is used.  17-32 rows that the verify kernel does not take
-    // stay on the decode kernel.
+    // workspace is used.  17-32 rows over fp16 / bf16 pools take the MFMA
+    // prefill kernel too (the decode kernel's two row tiles spill: 980 us
+    // against 470 us at config 5's batch); over int8 pools the verify kernel
+    // or else the decode kernel runs them.
     PrefillArgs pa;
     pa.q = q;
     pa.out = out;
@@ -178,7 +180,8 @@ static int paged_decode(const void* q, void* out, int q_dtype, const void* k_poo
     }
     if (nt != 0 && launch_verify_i8(pa, q_dtype, kv_dtype, scale_dtype, head_dim, stream))
       return check_launch("hpa_paged_decode");
-    if (nt != 2 && launch_prefill_mfma(pa, q_dtype, kv_dtype, scale_dtype, head_dim, q_per_seq, stream))
+    if ((nt != 2 || kv_dtype != HPA_I8) &&
+        launch_prefill_mfma(pa, q_dtype, kv_dtype, scale_dtype, head_dim, q_per_seq, stream))
       return check_launch("hpa_paged_decode");
     if (nt == 0) {
       const int st = launch_prefill_generic(pa, q_dtype, kv_dtype, scale_dtype, head_dim, q_per_seq, stream);

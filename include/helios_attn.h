@@ -85,9 +85,10 @@ size_t hpa_decode_workspace_size(int num_seqs, int q_per_seq, int num_q_heads, i
  * q_per_seq) is taken.  17-64 rows with fp16 queries over an int8 pool
  * (head_dim 64 or 128, block_size >= 16) run on a verify kernel that
  * dequantises in registers; it uses the workspace, when given, to cut long
- * contexts in two (fewer cuts with a smaller one).  Other shapes above 32
- * rows run on the prefill kernels (the MFMA one when it takes the shape:
- * fp16 / bf16 queries, head_dim 64 or 128, block_size >= 16), with the same
+ * contexts (fewer cuts with a smaller one).  Over fp16 / bf16 pools, 17 rows
+ * and more, and other shapes above 32 rows, run on the prefill kernels (the
+ * MFMA one when it takes the shape: fp16 / bf16 queries, head_dim 64 or
+ * 128, block_size >= 16; else above 32 rows the generic one), with the same
  * results as hpa_paged_prefill over the same tokens; the workspace is then
  * unused.
  * part_tokens: smallest share of the context, in tokens, one wave streams

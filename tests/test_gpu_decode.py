@@ -224,6 +224,23 @@ def test_verify_rows_and_gqa_groups(Hq, Hkv, T, quant):
     _check(got, want, torch.float16, f"verify {Hq}/{Hkv}x{T}")
 
 
+@pytest.mark.parametrize("Hq,Hkv,T,D,dtype", [(8, 2, 5, 128, torch.bfloat16), (16, 4, 8, 64, torch.float16),
+                                              (14, 2, 3, 128, torch.float16)])
+def test_verify_17_to_32_rows_on_fp_pools_runs_the_mfma_prefill_kernel(Hq, Hkv, T, D, dtype):
+    """17-32 query rows per KV head over fp16 / bf16 pools also go to the
+    MFMA prefill kernel (the decode kernel's two-row-tile instantiation
+    spills registers): bit for bit the same tokens through
+    paged_attention_varlen, and the oracle."""
+    print(f"verify {Hq}/{Hkv}x{T} D {D} {dtype} on the MFMA kernel", flush=True)
+    lens = [T, T + 5, 40, 129, 300, 1500]
+    cache, tables, q = _case(90 + Hq + T, len(lens), lens, Hq, Hkv, D, 16, dtype, q_per_seq=T)
+    got = paged_attention_verify_batched(q, cache, tables, lens, T)
+    same = paged_attention_varlen(q, cache, tables, [T] * len(lens), [c - T for c in lens], lens)
+    assert torch.equal(got, same)
+    want = R.paged_verify_batched(to_np(q).astype(np.float32), pool_of(cache), tables, lens, T)
+    _check(got, want, dtype, "17-32-row verify")
+
+
 @pytest.mark.parametrize("quant", [False, True])
 @pytest.mark.parametrize("Hq,Hkv,T,D,dtype", [(32, 4, 8, 128, torch.float16), (16, 4, 9, 128, torch.float16),
                                               (8, 1, 5, 128, torch.float16), (8, 1, 6, 64, torch.bfloat16)])
