@@ -162,20 +162,30 @@ struct AttnCore {
   // algebraically: S = 2^24 (S' - 128 2^-24 sum(q)) and O = O' - 1152 sum(P').
   // The small key offset keeps the fp32 sums of S' near the score's own
   // magnitude, so large key scales do not amplify their rounding.
-  static constexpr bool I8F16 = QUANT && std::is_same<CT, F16>::value;
+  //
+  // Over int8 pools the MFMAs run in fp16 for bf16 queries too (MT, the math
+  // type): a bf16 value is exact in fp16 within fp16's range, and each
+  // query row enters scaled by a power of two that brings its largest
+  // element below 2^15 (the scale returns in the row's score scale), so
+  // the cheap fp16 form of the dequantisation serves both.  The output is
+  // still written in the query dtype.
+  typedef typename std::conditional<QUANT && std::is_same<CT, BF16>::value, F16, CT>::type MT;
+  static constexpr bool I8F16 = QUANT && std::is_same<MT, F16>::value;
+  static constexpr bool kBf16Q = QUANT && std::is_same<CT, BF16>::value;
   static constexpr float kI8KOff = 0x1p-17f;  // 128 * 2^-24
   static constexpr float kI8VOff = 1152.f;
   // P enters the PV MFMAs as two terms (hi + lo) for bf16 compute and for
   // int8 pools with fp16 compute
-  static constexpr bool kSplitP = std::is_same<CT, BF16>::value || I8F16;
+  static constexpr bool kSplitP = std::is_same<MT, BF16>::value || I8F16;
   // Rescale the accumulators only when a row max grows by more than 2^8;
   // probabilities then stay below 2^8 relative to the running reference.
   static constexpr float kLazy = 8.f;
 
-  Frag<CT> q[NT][C];
+  Frag<MT> q[NT][C];
   f32x4 o[NT][J];
   f32x4 ps[NT];     // I8F16: sum over keys of the fp16 P' fed to the PV MFMAs
   float qoff[NT];   // I8F16: 128 * 2^-24 * sum_d q[row][d]
+  float qexp[NT];   // bf16 queries over int8: the power of two the row was scaled down by
   float m[NT], l[NT];
   int lim[NT];
 
@@ -227,6 +237,31 @@ struct AttnCore {
       l[nt] = 0.f;
 #pragma unroll
       for (int j = 0; j < J; ++j) o[nt][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+      qexp[nt] = 1.f;
+      if constexpr (kBf16Q) {
+        // bf16 bits -> fp16, the row scaled by 2^-e with e >= 0 the least
+        // that brings its largest magnitude below 2^15
+        float mx = 0.f;
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const uint32_t wi = q[nt][c].w[i];
+            mx = fmaxf(mx, fmaxf(fabsf(bf16_bits_to_f32(wi & 0xffffu)), fabsf(bf16_bits_to_f32(wi >> 16))));
+          }
+        mx = xor_max(mx);
+        const int e = mx >= 0x1p15f ? min(__builtin_amdgcn_frexp_expf(mx) - 15, 240) : 0;
+        qexp[nt] = __builtin_ldexpf(1.f, e);
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const uint32_t wi = q[nt][c].w[i];
+            const f16x2 h = {(_Float16)__builtin_ldexpf(bf16_bits_to_f32(wi & 0xffffu), -e),
+                             (_Float16)__builtin_ldexpf(bf16_bits_to_f32(wi >> 16), -e)};
+            q[nt][c].w[i] = __builtin_bit_cast(uint32_t, h);
+          }
+      }
       if constexpr (I8F16) {
         float sq = 0.f;
 #pragma unroll
@@ -445,10 +480,10 @@ struct AttnCore {
   }
 
   // K operand of one 16-key tile, chunk c, from its raw registers.
-  __device__ __forceinline__ static void k_frag(const uint32_t* kr, int c, Frag<CT>& f) {
+  __device__ __forceinline__ static void k_frag(const uint32_t* kr, int c, Frag<MT>& f) {
     if constexpr (QUANT) {
       const uint32_t w0 = kr[2 * c], w1 = kr[2 * c + 1];
-      if constexpr (std::is_same<CT, F16>::value) {
+      if constexpr (std::is_same<MT, F16>::value) {
         // [b0^0x80, 0x00, b1^0x80, 0x00] = fp16 ((128 + x0) 2^-24, (128 + x1) 2^-24)
         const uint32_t x0 = w0 ^ 0x80808080u, x1 = w1 ^ 0x80808080u;
         f.w[0] = __builtin_amdgcn_perm(0u, x0, 0x0C010C00u);
@@ -464,7 +499,7 @@ struct AttnCore {
         }
         frag_from_f32(f, x);
       }
-    } else if constexpr (std::is_same<CT, F32>::value) {
+    } else if constexpr (std::is_same<MT, F32>::value) {
 #pragma unroll
       for (int s = 0; s < 8; ++s) f.f[s] = __builtin_bit_cast(float, kr[8 * c + s]);
     } else {
@@ -473,9 +508,9 @@ struct AttnCore {
   }
 
   // V^T operand for MFMA j: element j of each of the 8 key slots.
-  __device__ __forceinline__ static void v_frag(const Raw& r, int j, Frag<CT>& f) {
+  __device__ __forceinline__ static void v_frag(const Raw& r, int j, Frag<MT>& f) {
     if constexpr (QUANT) {
-      if constexpr (std::is_same<CT, F16>::value) {
+      if constexpr (std::is_same<MT, F16>::value) {
         // fp16 (1152 + x) pairs; the offset leaves through ps[]
 #pragma unroll
         for (int p = 0; p < 4; ++p)
@@ -545,7 +580,7 @@ struct AttnCore {
       for (int nt = 0; nt < NT; ++nt) st[t][nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int c = 0; c < C; ++c) {
-        Frag<CT> kf;
+        Frag<MT> kf;
         k_frag(r.k[t], c, kf);
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) st[t][nt] = mma(kf, q[nt][c], st[t][nt]);
@@ -554,8 +589,8 @@ struct AttnCore {
     // probabilities of every n-tile first, then the PV products one V^T
     // fragment at a time (each converted once and used by every n-tile), so
     // at most one converted V fragment is live
-    Frag<CT> pf[NT];
-    Frag<CT> pl[NT];  // bf16 and int8 -> fp16: the low half of P
+    Frag<MT> pf[NT];
+    Frag<MT> pl[NT];  // bf16 and int8 -> fp16: the low half of P
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       float x[8];
@@ -564,7 +599,7 @@ struct AttnCore {
       for (int s = 0; s < 8; ++s) {
         float v = st[s >> 2][nt][s & 3];
         if constexpr (I8F16) v -= qoff[nt];
-        v *= (I8F16 ? scale_log2 * 0x1p24f : scale_log2) * scale_at(r.ks[s >> 2], s & 3);
+        v *= (I8F16 ? scale_log2 * 0x1p24f * qexp[nt] : scale_log2) * scale_at(r.ks[s >> 2], s & 3);
         if (masked) {
           const int key = k0 + 16 * (s >> 2) + 4 * g + (s & 3);
           v = key < lim[nt] ? v : -INFINITY;
@@ -606,12 +641,12 @@ struct AttnCore {
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
           const uint32_t hb = (pf[nt].w[s >> 1] >> (16 * (s & 1))) & 0xffffu;
-          lo[s] = x[s] - (std::is_same<CT, BF16>::value ? bf16_bits_to_f32(hb) : f16_bits_to_f32(hb));
+          lo[s] = x[s] - (std::is_same<MT, BF16>::value ? bf16_bits_to_f32(hb) : f16_bits_to_f32(hb));
         }
         frag_from_f32(pl[nt], lo);
       }
       if constexpr (I8F16) {
-        Frag<CT> ones;
+        Frag<MT> ones;
         ones.w = (u32x4){0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u};
         ps[nt] = mma(ones, pf[nt], ps[nt]);
         ps[nt] = mma(ones, pl[nt], ps[nt]);
@@ -619,7 +654,7 @@ struct AttnCore {
     }
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-      Frag<CT> vf;
+      Frag<MT> vf;
       v_frag(r, j, vf);
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
