@@ -46,6 +46,7 @@
 namespace hpa {
 
 typedef float f32x16v __attribute__((ext_vector_type(16)));
+typedef __bf16 vi_bf16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kViWaves = 2;    // 32 rows each
 constexpr int kViStages = 4;   // LDS stages; copies run kViStages - 1 steps ahead
@@ -162,7 +163,11 @@ __device__ __forceinline__ float vi_fma_scale(float x, const uint32_t* w, int e,
   else return __builtin_fmaf(x, __builtin_bit_cast(float, w[e]), c);
 }
 
-template <class ST, int D>
+// BQ: bf16 queries and output.  The MFMAs still run in fp16: a bf16 value is
+// exact in fp16 within fp16's range, each query row enters scaled by the
+// power of two that brings its largest element below 2^15, and that scale
+// returns in the row's score scale.
+template <class ST, int D, bool BQ>
 __global__ __launch_bounds__(64 * kViWaves, 2) void verify_i8_kernel(const PrefillArgs a) {
   constexpr int CH = D / 16;                     // 16-byte chunks per key row (int8)
   constexpr int DB = D / 32;                     // O^T blocks of 32 dims
@@ -277,14 +282,37 @@ __global__ __launch_bounds__(64 * kViWaves, 2) void verify_i8_kernel(const Prefi
   u32x4 qf[CH];
   float qs = 0.f;
 #pragma unroll
-  for (int c = 0; c < CH; ++c) {
-    qf[c] = rv ? *reinterpret_cast<const u32x4*>(qrow + 16 * c + 8 * h) : (u32x4){0, 0, 0, 0};
+  for (int c = 0; c < CH; ++c) qf[c] = rv ? *reinterpret_cast<const u32x4*>(qrow + 16 * c + 8 * h) : (u32x4){0, 0, 0, 0};
+  float qexp = 1.f;  // bf16: the power of two the row was scaled down by
+  if constexpr (BQ) {
+    float mx = 0.f;
+#pragma unroll
+    for (int c = 0; c < CH; ++c)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t wd = qf[c][e];
+        mx = fmaxf(mx, fmaxf(fabsf(bf16_bits_to_f32(wd & 0xffffu)), fabsf(bf16_bits_to_f32(wd >> 16))));
+      }
+    mx = vi_pair_max(mx);
+    const int ex = mx >= 0x1p15f ? min(__builtin_amdgcn_frexp_expf(mx) - 15, 240) : 0;
+    qexp = __builtin_ldexpf(1.f, ex);
+#pragma unroll
+    for (int c = 0; c < CH; ++c)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t wd = qf[c][e];
+        const f16x2 hv = {(_Float16)__builtin_ldexpf(bf16_bits_to_f32(wd & 0xffffu), -ex),
+                          (_Float16)__builtin_ldexpf(bf16_bits_to_f32(wd >> 16), -ex)};
+        qf[c][e] = __builtin_bit_cast(uint32_t, hv);
+      }
+  }
+#pragma unroll
+  for (int c = 0; c < CH; ++c)
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const uint32_t wd = qf[c][e];
       qs += f16_bits_to_f32(wd & 0xffffu) + f16_bits_to_f32(wd >> 16);
     }
-  }
   // the first S' MFMA of a step starts from -128 sum(q) 2^-24, so the score
   // times 2^-24 leaves the accumulator directly
   const float qoff = 0x1p-17f * vi_pair_sum(qs);
@@ -375,7 +403,7 @@ __global__ __launch_bounds__(64 * kViWaves, 2) void verify_i8_kernel(const Prefi
 #pragma unroll
   for (int db = 0; db < DB; ++db) o[db] = (f32x16v){};
   float m = -INFINITY, l = 0.f, loff = 0.f;
-  const float cs = a.scale_log2 * 0x1p24f;  // the scores arrive times 2^-24
+  const float cs = a.scale_log2 * 0x1p24f * qexp;  // the scores arrive times 2^-24 (and 2^-e)
 
   auto step = [&](int i) {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
@@ -618,20 +646,26 @@ __global__ __launch_bounds__(64 * kViWaves, 2) void verify_i8_kernel(const Prefi
 #pragma unroll
       for (int v4 = 0; v4 < 4; ++v4) {
         u32x2 pk;
-        pk[0] = __builtin_bit_cast(uint32_t, (f16x2){(_Float16)(o[db][4 * v4] * inv), (_Float16)(o[db][4 * v4 + 1] * inv)});
-        pk[1] = __builtin_bit_cast(uint32_t,
-                                   (f16x2){(_Float16)(o[db][4 * v4 + 2] * inv), (_Float16)(o[db][4 * v4 + 3] * inv)});
+        const float e0 = o[db][4 * v4] * inv, e1 = o[db][4 * v4 + 1] * inv;
+        const float e2 = o[db][4 * v4 + 2] * inv, e3 = o[db][4 * v4 + 3] * inv;
+        if constexpr (BQ) {
+          pk[0] = __builtin_bit_cast(uint32_t, (vi_bf16x2){(__bf16)e0, (__bf16)e1});
+          pk[1] = __builtin_bit_cast(uint32_t, (vi_bf16x2){(__bf16)e2, (__bf16)e3});
+        } else {
+          pk[0] = __builtin_bit_cast(uint32_t, (f16x2){(_Float16)e0, (_Float16)e1});
+          pk[1] = __builtin_bit_cast(uint32_t, (f16x2){(_Float16)e2, (_Float16)e3});
+        }
         *reinterpret_cast<u32x2*>(orow + 32 * db + 8 * v4) = pk;
       }
   }
 }
 
-template <class ST, int D>
+template <class ST, int D, bool BQ>
 static void vi_launch(PrefillArgs a, long units, hipStream_t s) {
   static int per_cu = 0;  // workgroups resident per CU
   if (!per_cu) {
     int nb = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void*>(&verify_i8_kernel<ST, D>),
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void*>(&verify_i8_kernel<ST, D, BQ>),
                                                      64 * kViWaves, 0) != hipSuccess || nb <= 0)
       nb = 1;
     per_cu = nb;
@@ -658,25 +692,26 @@ static void vi_launch(PrefillArgs a, long units, hipStream_t s) {
   // cutting: every XCD gets enough workgroups for every item: nk + budget
   // with two pieces per cut unit, at most xcd_slots with more
   const dim3 grid((unsigned)(cut ? 8 * std::max<long>(nk + budget, xcd_slots) : units)), block(64 * kViWaves);
-  hipLaunchKernelGGL((verify_i8_kernel<ST, D>), grid, block, 0, s, a);
+  hipLaunchKernelGGL((verify_i8_kernel<ST, D, BQ>), grid, block, 0, s, a);
 }
 
 bool launch_verify_i8(const PrefillArgs& a, int q_dtype, int kv_dtype, int scale_dtype, int head_dim,
                       hipStream_t s) {
-  if (q_dtype != HPA_F16 || kv_dtype != HPA_I8 || !a.ks || !a.vs || a.uniform_q <= 0) return false;
+  if ((q_dtype != HPA_F16 && q_dtype != HPA_BF16) || kv_dtype != HPA_I8 || !a.ks || !a.vs || a.uniform_q <= 0)
+    return false;
   if (a.bs_log2 < 4 || (head_dim != 64 && head_dim != 128)) return false;
   const long rows = (long)a.uniform_q * a.group;
   if (rows <= 16 || rows > 32 * kViWaves) return false;
   const long units = (long)a.num_seqs * a.num_kv_heads;
   if (units <= 0 || units > 0x3fffffffL) return false;
-  if (scale_dtype == HPA_F16) {
-    if (head_dim == 128) vi_launch<F16, 128>(a, units, s);
-    else vi_launch<F16, 64>(a, units, s);
-  } else if (scale_dtype == HPA_F32) {
-    if (head_dim == 128) vi_launch<F32, 128>(a, units, s);
-    else vi_launch<F32, 64>(a, units, s);
+  if (scale_dtype != HPA_F16 && scale_dtype != HPA_F32) return false;
+  const bool f16s = scale_dtype == HPA_F16, bq = q_dtype == HPA_BF16;
+  if (head_dim == 128) {
+    if (f16s) bq ? vi_launch<F16, 128, true>(a, units, s) : vi_launch<F16, 128, false>(a, units, s);
+    else bq ? vi_launch<F32, 128, true>(a, units, s) : vi_launch<F32, 128, false>(a, units, s);
   } else {
-    return false;
+    if (f16s) bq ? vi_launch<F16, 64, true>(a, units, s) : vi_launch<F16, 64, false>(a, units, s);
+    else bq ? vi_launch<F32, 64, true>(a, units, s) : vi_launch<F32, 64, false>(a, units, s);
   }
   return true;
 }

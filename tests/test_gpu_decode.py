@@ -165,6 +165,28 @@ def test_int8_kv(scale_dtype, D, dtype):
     _check(got, _oracle_decode(cache, q, tables, lens), dtype, f"int8 D={D}")
 
 
+@pytest.mark.parametrize("T,scale_dtype", [(1, torch.float16), (3, torch.float16), (5, torch.float16),
+                                           (8, torch.float32), (12, torch.float16)])
+def test_bf16_queries_over_int8_pools(T, scale_dtype):
+    """bf16 queries over an int8 pool run the fp16 MFMA form: each query
+    row enters fp16 scaled by the power of two that brings its largest
+    element below 2^15.  Rows of ordinary magnitude, rows of 2^17 and rows
+    with elements down to 2^-30 (fp16 subnormals and below) all match the
+    oracle; 4 * T rows per KV head cover the decode kernel's one- and
+    two-tile forms and the wide verify kernel (20, 32 and 48 rows)."""
+    print(f"bf16 queries over int8, q_per_seq {T}, scales {scale_dtype}", flush=True)
+    lens = [T, 40, 300, 1100]
+    cache, tables, q = _case(170 + T, len(lens), lens, 16, 4, 128, 16, torch.bfloat16, quant=True,
+                             scale_dtype=scale_dtype, q_per_seq=T)
+    q = q.float()
+    q[0::3] *= 2.0 ** 17 / 8  # large rows: scores in the thousands, one key dominates
+    q[1::3, :, ::2] *= 2.0 ** -28  # tiny elements next to ordinary ones
+    q = q.to(torch.bfloat16)
+    got = paged_attention_verify_batched(q, cache, tables, lens, T) if T > 1 else \
+        paged_attention_decode_batched(q, cache, tables, lens)
+    _check(got, _oracle_decode(cache, q, tables, lens, q_per_seq=T), torch.bfloat16, "bf16 over int8")
+
+
 def _scale_range(cache, seed):
     """Key scales from 2^-14 to 2^4 and value scales from 2^-14 to 2^-6,
     drawn per block (the payload keeps its bytes)."""
@@ -247,20 +269,22 @@ def test_verify_17_to_32_rows_on_fp_pools_runs_the_mfma_prefill_kernel(Hq, Hkv, 
 def test_wide_verify_runs_the_mfma_prefill_kernel(Hq, Hkv, T, D, dtype, quant):
     """33-64 query rows per KV head go to the MFMA prefill kernel: the
     verify equals, bit for bit, the same tokens through paged_attention_varlen
-    (start = context - T), and the oracle.  On int8 pools that kernel attends
-    over the dequantised values rounded to the compute dtype, as helios'
-    gather hands them over (paged_attn.py:213-235), so the oracle reads the
-    same values.  fp16 queries over int8 pools take the register-dequantising
-    verify kernel instead (test_int8_wide_verify_dequantises_in_registers)."""
+    (start = context - T), and the oracle.  Queries over int8 pools take the
+    register-dequantising verify kernel instead, which keeps the dequantised
+    values in fp32 as the decode kernel does: it matches the exact oracle,
+    and for fp16, to the bound, the oracle over the dequantised values rounded
+    to the compute dtype as helios' gather hands them over
+    (paged_attn.py:213-235).  Rounding those values to bf16 moves scores by
+    more than the bound, so bf16 is held to the exact oracle alone."""
     print(f"wide verify {Hq}/{Hkv}x{T} D {D} {dtype} int8 {quant}", flush=True)
     lens = [T, T + 5, 40, 129, 300]
     cache, tables, q = _case(80 + Hq + T, len(lens), lens, Hq, Hkv, D, 16, dtype,
                              quant=quant, q_per_seq=T)
     got = paged_attention_verify_batched(q, cache, tables, lens, T)
-    if quant and dtype == torch.float16:
-        # the verify kernel keeps the dequantised values in fp32, as the
-        # decode kernel does; both oracles agree with it to the bound
+    if quant:
         _check(got, _oracle_decode(cache, q, tables, lens, q_per_seq=T), dtype, "int8 wide verify")
+        if dtype == torch.bfloat16:
+            return
     else:
         same = paged_attention_varlen(q, cache, tables, [T] * len(lens), [c - T for c in lens], lens)
         assert torch.equal(got, same)
