@@ -239,8 +239,9 @@ struct AttnCore {
       for (int j = 0; j < J; ++j) o[nt][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
       qexp[nt] = 1.f;
       if constexpr (kBf16Q) {
-        // bf16 bits -> fp16, the row scaled by 2^-e with e >= 0 the least
-        // that brings its largest magnitude below 2^15
+        // bf16 bits -> fp16, the row scaled by the power of two 2^-e that
+        // brings its largest magnitude into [2^14, 2^15): the fp16 row then
+        // keeps the bf16 precision of every element down to 2^-28 of it
         float mx = 0.f;
 #pragma unroll
         for (int c = 0; c < C; ++c)
@@ -250,7 +251,7 @@ struct AttnCore {
             mx = fmaxf(mx, fmaxf(fabsf(bf16_bits_to_f32(wi & 0xffffu)), fabsf(bf16_bits_to_f32(wi >> 16))));
           }
         mx = xor_max(mx);
-        const int e = mx >= 0x1p15f ? min(__builtin_amdgcn_frexp_expf(mx) - 15, 240) : 0;
+        const int e = mx > 0.f ? max(min(__builtin_amdgcn_frexp_expf(mx) - 15, 240), -120) : 0;
         qexp[nt] = __builtin_ldexpf(1.f, e);
 #pragma unroll
         for (int c = 0; c < C; ++c)

@@ -165,8 +165,8 @@ __device__ __forceinline__ float vi_fma_scale(float x, const uint32_t* w, int e,
 
 // BQ: bf16 queries and output.  The MFMAs still run in fp16: a bf16 value is
 // exact in fp16 within fp16's range, each query row enters scaled by the
-// power of two that brings its largest element below 2^15, and that scale
-// returns in the row's score scale.
+// power of two that brings its largest element into [2^14, 2^15), and that
+// scale returns in the row's score scale.
 template <class ST, int D, bool BQ>
 __global__ __launch_bounds__(64 * kViWaves, 2) void verify_i8_kernel(const PrefillArgs a) {
   constexpr int CH = D / 16;                     // 16-byte chunks per key row (int8)
@@ -294,7 +294,7 @@ __global__ __launch_bounds__(64 * kViWaves, 2) void verify_i8_kernel(const Prefi
         mx = fmaxf(mx, fmaxf(fabsf(bf16_bits_to_f32(wd & 0xffffu)), fabsf(bf16_bits_to_f32(wd >> 16))));
       }
     mx = vi_pair_max(mx);
-    const int ex = mx >= 0x1p15f ? min(__builtin_amdgcn_frexp_expf(mx) - 15, 240) : 0;
+    const int ex = mx > 0.f ? max(min(__builtin_amdgcn_frexp_expf(mx) - 15, 240), -120) : 0;
     qexp = __builtin_ldexpf(1.f, ex);
 #pragma unroll
     for (int c = 0; c < CH; ++c)

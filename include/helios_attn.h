@@ -82,8 +82,8 @@ size_t hpa_decode_workspace_size(int num_seqs, int q_per_seq, int num_q_heads, i
  * (helios' causal rule, paged_attn.py:401-404, with start_pos = context -
  * q_per_seq).  An empty context yields zeros.  Softmax scale sm_scale.
  * Any number of query rows per KV head ((num_q_heads / num_kv_heads) *
- * q_per_seq) is taken.  17-64 rows with fp16 queries over an int8 pool
- * (head_dim 64 or 128, block_size >= 16) run on a verify kernel that
+ * q_per_seq) is taken.  17-64 rows with fp16 or bf16 queries over an int8
+ * pool (head_dim 64 or 128, block_size >= 16) run on a verify kernel that
  * dequantises in registers; it uses the workspace, when given, to cut long
  * contexts (fewer cuts with a smaller one).  Over fp16 / bf16 pools, 17 rows
  * and more, and other shapes above 32 rows, run on the prefill kernels (the

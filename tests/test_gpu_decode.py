@@ -170,9 +170,9 @@ def test_int8_kv(scale_dtype, D, dtype):
 def test_bf16_queries_over_int8_pools(T, scale_dtype):
     """bf16 queries over an int8 pool run the fp16 MFMA form: each query
     row enters fp16 scaled by the power of two that brings its largest
-    element below 2^15.  Rows of ordinary magnitude, rows of 2^17 and rows
-    with elements down to 2^-30 (fp16 subnormals and below) all match the
-    oracle; 4 * T rows per KV head cover the decode kernel's one- and
+    element into [2^14, 2^15).  Rows of ordinary magnitude, rows of 2^14,
+    rows with elements down to 2^-30 and rows of 2^-40 throughout (all below
+    fp16's range unscaled) match the oracle; 4 * T rows per KV head cover the decode kernel's one- and
     two-tile forms and the wide verify kernel (20, 32 and 48 rows)."""
     print(f"bf16 queries over int8, q_per_seq {T}, scales {scale_dtype}", flush=True)
     lens = [T, 40, 300, 1100]
@@ -181,6 +181,7 @@ def test_bf16_queries_over_int8_pools(T, scale_dtype):
     q = q.float()
     q[0::3] *= 2.0 ** 17 / 8  # large rows: scores in the thousands, one key dominates
     q[1::3, :, ::2] *= 2.0 ** -28  # tiny elements next to ordinary ones
+    q[2::3, ::2] *= 2.0 ** -40  # whole heads far below fp16's range
     q = q.to(torch.bfloat16)
     got = paged_attention_verify_batched(q, cache, tables, lens, T) if T > 1 else \
         paged_attention_decode_batched(q, cache, tables, lens)
