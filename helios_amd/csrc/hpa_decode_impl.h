@@ -54,7 +54,7 @@ struct DecodeArgs {
   int min_steps;   // lower bound on a wave's slice, in 32-key steps
   int* counters;   // [num_seqs * Hkv] arrival counters, zero between calls
   float* ws_ml;    // [W][2][rows][2]  (m, l) of partial pieces
-  float* ws_o;     // [W][2][rows][D]  unnormalised O of partial pieces
+  float* ws_o;     // [W][2][NT][J][64 lanes][4]  unnormalised O of partial pieces
 };
 
 constexpr int kWavesPerGroup = 4;
@@ -64,6 +64,11 @@ constexpr int kWaveCap = 4096;          // 256 CUs x 16 resident waves
 // younger one finishes long after the older, while a single wave with a deep
 // pipeline keeps the SIMD's share of HBM busy on its own.
 constexpr int kDepth = 3;
+// head_dim 256 keeps one step in flight: a step's K/V registers (64 VGPRs per
+// tensor for 16-bit pools) times a ring of four spilled over a thousand
+// registers to scratch, which cost two thirds of the bandwidth
+template <int D>
+constexpr int ring_depth() { return D >= 256 ? 1 : kDepth; }
 constexpr int kDefaultMinTokens = 256;  // per-wave slice floor (8 steps)
 // What a unit costs beyond its steps, in step-equivalents: its prologue
 // (table window, query rows, first loads in flight) and epilogue (output or
@@ -225,7 +230,9 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
   typedef AttnCore<CT, KVT, ST, D, NT> Core;
   typedef typename CT::storage q_t;
   constexpr int J = Core::J;
-  constexpr int kMergeBatch = J <= 4 ? 4 : 2;  // split-K pieces loaded per round trip of a merge
+  // split-K pieces loaded per round trip of a merge (one piece of 16 rows
+  // at head_dim 256 is 64 VGPRs)
+  constexpr int kMergeBatch = J <= 4 ? 4 : J <= 8 ? 2 : 1;
   const int wave = __builtin_amdgcn_readfirstlane(blockIdx.x * kWavesPerGroup + (threadIdx.x >> 6));
   if (wave >= a.num_waves) return;
   const int lane = threadIdx.x & 63, n = lane & 15, g = lane >> 4;
@@ -252,9 +259,10 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
   u.kvh = head;
 
   const typename Core::LaneOff lo = Core::lane_off();
-  constexpr int NB = kDepth + 1;
-  // A ring of kDepth + 1 register buffers, unrolled so every index is a
-  // compile-time constant: kDepth steps of loads stay in flight while a step
+  constexpr int DEP = ring_depth<D>();
+  constexpr int NB = DEP + 1;
+  // A ring of DEP + 1 register buffers, unrolled so every index is a
+  // compile-time constant: DEP steps of loads stay in flight while a step
   // computes, and no buffer is ever copied (a register copy of data still in
   // flight would make the compiler wait for it).
   typename Core::Raw rb[NB];
@@ -309,11 +317,11 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
   };
   auto issue_first = [&](const PoolView& v, TableWindow& w, int first, int end) {
 #pragma unroll
-    for (int k = 0; k < kDepth; ++k) load_step(v, w, 32 * (first + k), rb[k], first + k < end);
+    for (int k = 0; k < DEP; ++k) load_step(v, w, 32 * (first + k), rb[k], first + k < end);
   };
 
   // ---- the first unit: its query rows, its table window, then its first
-  // kDepth steps of loads (in that order: waiting for the rows does not wait
+  // DEP steps of loads (in that order: waiting for the rows does not wait
   // for the K/V steps behind them)
   int lbeg = (int)max(s0 - (u.g + kUnitCost), 0L);  // first local step of the unit in the slice
   long sb = u.g + kUnitCost;  // global position of the unit's step 0
@@ -354,7 +362,7 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
       if (BIG) stage_window(lds_wnext, a.tables + (long)(u.b + 1) * a.table_stride, a.table_stride, 0);
     }
 
-    // ---- stream the unit's steps [lbeg, lend); the first kDepth are in flight
+    // ---- stream the unit's steps [lbeg, lend); the first DEP are in flight
     if (ctx > 0) {
       bool done = false;
       for (int st = lbeg; !done; st += NB) {
@@ -362,7 +370,7 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
         for (int k = 0; k < NB; ++k) {
           if (!done) {
             const int cur = st + k;
-            load_step(pv, win, 32 * (cur + kDepth), rb[(k + kDepth) % NB], cur + kDepth < lend);
+            load_step(pv, win, 32 * (cur + DEP), rb[(k + DEP) % NB], cur + DEP < lend);
             core.compute(rb[k], 32 * cur, a.scale_log2, 32 * cur + 32 > minlim, ctx);
             done = cur + 1 >= lend;
           }
@@ -370,7 +378,7 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
       }
     }
 
-    // ---- the next unit's query rows, window and first kDepth steps of loads
+    // ---- the next unit's query rows, window and first DEP steps of loads
     // go out before this unit's epilogue, so they overlap its latency.  The
     // loads still in flight are this unit's trailing empty prefetches and
     // its staged window, long landed: waiting for them costs little.
@@ -430,6 +438,14 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
     // stored -- and every other from the workspace, so the result does not
     // depend on which wave merges.
     const __amdgpu_buffer_rsrc_t ro = ws_rsrc(a.ws_o), rml = ws_rsrc(a.ws_ml);
+    // A piece's O is stored lane-major: chunk c of n-tile nt of slot sl holds
+    // the 16 bytes of every lane in lane order, so each store (and load)
+    // instruction moves 1 KB of consecutive bytes.  Row-major pieces made
+    // each instruction 48 partial-line writes through to the coherence
+    // point, several microseconds per published piece under the K/V stream.
+    auto o_chunk = [&](long sl, int nt) -> uint32_t {
+      return (uint32_t)(((sl * NT + nt) * J * 64 + lane) * 16);
+    };
     auto merge_pieces = [&](const UnitPos& uu, int wa_, int wb_, long slot_a_) {
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
@@ -461,12 +477,10 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
             const long sl = p == wa_ ? slot_a_ : 2L * (p * H + head);
             ml[k] = __builtin_amdgcn_raw_buffer_load_b64(rml, ld ? (uint32_t)((sl * a.rows + r) * 8) : kPastRecords,
                                                          0, kCoherent);
-            const uint32_t ob = (uint32_t)(((sl * a.rows + r) * D + 4 * J * g) * 4);
+            const uint32_t ob = o_chunk(sl, nt);
 #pragma unroll
             for (int c = 0; c < J; ++c)
-              ov[k][c] = 4 * J * g + 4 * c < D
-                             ? __builtin_amdgcn_raw_buffer_load_b128(ro, ld ? ob + 16 * c : kPastRecords, 0, kCoherent)
-                             : (u32x4){0, 0, 0, 0};
+              ov[k][c] = __builtin_amdgcn_raw_buffer_load_b128(ro, ld ? ob + 1024 * c : kPastRecords, 0, kCoherent);
           }
 #pragma unroll
           for (int k = 0; k < kMergeBatch; ++k) {
@@ -533,26 +547,25 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
           const int r = nt * 16 + n;
-          if (r < a.rows) {
-            // the lane's 4J dims are contiguous from 4Jg, element (j, i) at J*i + j
-            float tmp[4 * J];
+          // every lane stores (rows past a.rows and dims past D hold values
+          // no merge uses), so each instruction writes whole cache lines;
+          // the lane's 4J dims are contiguous from 4Jg, element (j, i) at J*i + j
+          float tmp[4 * J];
 #pragma unroll
-            for (int j = 0; j < J; ++j)
+          for (int j = 0; j < J; ++j)
 #pragma unroll
-              for (int i = 0; i < 4; ++i) tmp[J * i + j] = core.out_val(nt, j, i);
-            const uint32_t ob = (uint32_t)(((slot * a.rows + r) * D + 4 * J * g) * 4);
+            for (int i = 0; i < 4; ++i) tmp[J * i + j] = core.out_val(nt, j, i);
+          const uint32_t ob = o_chunk(slot, nt);
 #pragma unroll
-            for (int c = 0; c < J; ++c)
-              if (4 * J * g + 4 * c < D)
-                __builtin_amdgcn_raw_buffer_store_b128(
-                    (u32x4){__builtin_bit_cast(uint32_t, tmp[4 * c]), __builtin_bit_cast(uint32_t, tmp[4 * c + 1]),
-                            __builtin_bit_cast(uint32_t, tmp[4 * c + 2]), __builtin_bit_cast(uint32_t, tmp[4 * c + 3])},
-                    ro, ob + 16 * c, 0, kCoherent);
-            if (g == 0)
-              __builtin_amdgcn_raw_buffer_store_b64(
-                  (u32x2){__builtin_bit_cast(uint32_t, core.m[nt]), __builtin_bit_cast(uint32_t, lrow[nt])}, rml,
-                  (uint32_t)((slot * a.rows + r) * 8), 0, kCoherent);
-          }
+          for (int c = 0; c < J; ++c)
+            __builtin_amdgcn_raw_buffer_store_b128(
+                (u32x4){__builtin_bit_cast(uint32_t, tmp[4 * c]), __builtin_bit_cast(uint32_t, tmp[4 * c + 1]),
+                        __builtin_bit_cast(uint32_t, tmp[4 * c + 2]), __builtin_bit_cast(uint32_t, tmp[4 * c + 3])},
+                ro, ob + 1024 * c, 0, kCoherent);
+          if (r < a.rows && g == 0)
+            __builtin_amdgcn_raw_buffer_store_b64(
+                (u32x2){__builtin_bit_cast(uint32_t, core.m[nt]), __builtin_bit_cast(uint32_t, lrow[nt])}, rml,
+                (uint32_t)((slot * a.rows + r) * 8), 0, kCoherent);
         }
         // count it in once its stores are complete (hence visible device-wide)
         __atomic_signal_fence(__ATOMIC_SEQ_CST);

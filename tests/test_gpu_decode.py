@@ -154,6 +154,23 @@ def test_head_dims_and_dtypes(D, dtype):
     _check(got, _oracle_decode(cache, q, tables, lens), dtype, f"D={D} {dtype}")
 
 
+@pytest.mark.parametrize("quant", [False, True])
+@pytest.mark.parametrize("dtype,T", [(torch.float16, 1), (torch.bfloat16, 1), (torch.float16, 5),
+                                     (torch.bfloat16, 12)])
+def test_head_dim_256_split_k(dtype, T, quant):
+    """head_dim 256 keeps one step of loads in flight and merges one piece
+    per round trip; long contexts cut into many 128-token pieces exercise
+    the merge, and 4 * T rows per KV head the one-, two- and four-tile
+    forms (no other kernel takes head_dim 256)."""
+    print(f"head_dim 256, {dtype}, q_per_seq {T}, int8 {quant}", flush=True)
+    lens = [T, 40, 700, 2100, 4500]
+    cache, tables, q = _case(260 + T, len(lens), lens, 8, 2, 256, 16, dtype, quant=quant, q_per_seq=T)
+    ks, vs = cache._scales()
+    got = paged_attention_decode_hip(q, cache.k_cache, cache.v_cache, tables, lens, 1 / 16, ks, vs,
+                                     q_per_seq=T, part_tokens=128)
+    _check(got, _oracle_decode(cache, q, tables, lens, q_per_seq=T, scale=1 / 16), dtype, "D=256")
+
+
 @pytest.mark.parametrize("scale_dtype", [torch.float16, torch.float32])
 @pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
