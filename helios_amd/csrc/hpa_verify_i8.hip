@@ -548,7 +548,11 @@ __global__ __launch_bounds__(64 * kViWaves, 2) void verify_i8_kernel(const Prefi
     // without publishing.
     const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(a.pieces, (short)0, 0x7fffffff, 0x00020000);
     const int li = 64 * w + lane;
-    const uint32_t uo = (uint32_t)li * 256u, mlo = (uint32_t)(2 * 64 * 64 + 2 * li) * 4u;
+    // O is stored lane-major: 16-byte chunk (db, c) of every lane of the
+    // workgroup in lane order, so each store and load instruction moves 1 KB
+    // of consecutive bytes rather than 64 partial cache lines
+    auto uo = [&](int db, int c) { return (uint32_t)(((db * 4 + c) * 128 + li) * 16); };
+    const uint32_t mlo = (uint32_t)(2 * 64 * 64 + 2 * li) * 4u;
     auto slot_off = [&](int p) { return (uint32_t)((slot + p) * kViSlotFloats) * 4u; };
     int* ctr = a.counters + unit;
     if (threadIdx.x == 0) s_red[0] = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -567,7 +571,7 @@ __global__ __launch_bounds__(64 * kViWaves, 2) void verify_i8_kernel(const Prefi
           __builtin_amdgcn_raw_buffer_store_b128(
               (u32x4){__builtin_bit_cast(uint32_t, e0), __builtin_bit_cast(uint32_t, e1),
                       __builtin_bit_cast(uint32_t, e2), __builtin_bit_cast(uint32_t, e3)},
-              pr, own + uo + 64 * db + 16 * c, 0, kViCoherent);
+              pr, own + uo(db, c), 0, kViCoherent);
         }
       __builtin_amdgcn_raw_buffer_store_b64((u32x2){__builtin_bit_cast(uint32_t, m), __builtin_bit_cast(uint32_t, lt)},
                                             pr, own + mlo, 0, kViCoherent);
@@ -622,8 +626,7 @@ __global__ __launch_bounds__(64 * kViWaves, 2) void verify_i8_kernel(const Prefi
             f32x16v u;
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-              const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(pr, slot_off(p) + uo + 64 * db + 16 * c, 0,
-                                                                    kViCoherent);
+              const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(pr, slot_off(p) + uo(db, c), 0, kViCoherent);
 #pragma unroll
               for (int e = 0; e < 4; ++e) {
                 const uint32_t xe = x[e];
