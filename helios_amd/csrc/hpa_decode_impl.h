@@ -439,12 +439,14 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
     // depend on which wave merges.
     const __amdgpu_buffer_rsrc_t ro = ws_rsrc(a.ws_o), rml = ws_rsrc(a.ws_ml);
     // A piece's O is stored lane-major: chunk c of n-tile nt of slot sl holds
-    // the 16 bytes of every lane in lane order, so each store (and load)
-    // instruction moves 1 KB of consecutive bytes.  Row-major pieces made
-    // each instruction 48 partial-line writes through to the coherence
-    // point, several microseconds per published piece under the K/V stream.
+    // the 16 bytes of each lane of a row below a.rows, lane (n, g) at g rt + n
+    // (rt rows in the tile), so each store (and load) instruction moves
+    // 64 rt consecutive bytes.  Row-major pieces made each instruction 48
+    // partial-line writes through to the coherence point, several
+    // microseconds per published piece under the K/V stream.
     auto o_chunk = [&](long sl, int nt) -> uint32_t {
-      return (uint32_t)(((sl * NT + nt) * J * 64 + lane) * 16);
+      const int rt = min(16, a.rows - 16 * nt);
+      return (uint32_t)(((sl * NT + nt) * J * 64 + g * rt + n) * 16);
     };
     auto merge_pieces = [&](const UnitPos& uu, int wa_, int wb_, long slot_a_) {
 #pragma unroll
@@ -547,9 +549,9 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
           const int r = nt * 16 + n;
-          // every lane stores (rows past a.rows and dims past D hold values
-          // no merge uses), so each instruction writes whole cache lines;
-          // the lane's 4J dims are contiguous from 4Jg, element (j, i) at J*i + j
+          if (r >= a.rows) continue;
+          // the lane's 4J dims are contiguous from 4Jg, element (j, i) at
+          // J*i + j (dims past D hold values no merge uses)
           float tmp[4 * J];
 #pragma unroll
           for (int j = 0; j < J; ++j)
@@ -562,7 +564,7 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
                 (u32x4){__builtin_bit_cast(uint32_t, tmp[4 * c]), __builtin_bit_cast(uint32_t, tmp[4 * c + 1]),
                         __builtin_bit_cast(uint32_t, tmp[4 * c + 2]), __builtin_bit_cast(uint32_t, tmp[4 * c + 3])},
                 ro, ob + 1024 * c, 0, kCoherent);
-          if (r < a.rows && g == 0)
+          if (g == 0)
             __builtin_amdgcn_raw_buffer_store_b64(
                 (u32x2){__builtin_bit_cast(uint32_t, core.m[nt]), __builtin_bit_cast(uint32_t, lrow[nt])}, rml,
                 (uint32_t)((slot * a.rows + r) * 8), 0, kCoherent);
