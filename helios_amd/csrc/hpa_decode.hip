@@ -37,16 +37,16 @@ static DecodePlan plan_decode(int num_seqs, int num_kv_heads, int max_context_le
 }
 
 // Workspace layout: a fixed region of kMaxUnits int32 arrival counters (one
-// per (sequence, KV head)), then (m, l) [W][2][rows][2] and O in fp32, whole
-// 16-row tiles of max(head_dim, 16) dims ([W][2][NT][J][64 lanes][4]).  The
-// counters sit at the same place whatever the shapes, so a zero-filled
-// workspace stays valid across calls of any shape.
+// per (sequence, KV head)), then (m, l) [W][2][rows][2] and O
+// [W][2][rows][max(head_dim, 16)] in fp32.  The counters sit at the same
+// place whatever the shapes, so a zero-filled workspace stays valid across
+// calls of any shape.
 constexpr long kMaxUnits = 1L << 18;
 constexpr size_t kCounterBytes = kMaxUnits * sizeof(int);
 static size_t ws_bytes(int waves, int rows, int head_dim) {
   if (waves <= 1) return 0;
   const size_t ml = (size_t)waves * 2 * rows * 2 * sizeof(float);
-  const size_t o = (size_t)waves * 2 * (16 * decode_nt(rows)) * std::max(head_dim, 16) * sizeof(float);
+  const size_t o = (size_t)waves * 2 * rows * std::max(head_dim, 16) * sizeof(float);
   return kCounterBytes + ml + o;
 }
 

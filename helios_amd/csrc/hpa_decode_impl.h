@@ -54,7 +54,7 @@ struct DecodeArgs {
   int min_steps;   // lower bound on a wave's slice, in 32-key steps
   int* counters;   // [num_seqs * Hkv] arrival counters, zero between calls
   float* ws_ml;    // [W][2][rows][2]  (m, l) of partial pieces
-  float* ws_o;     // [W][2][NT][J][64 lanes][4]  unnormalised O of partial pieces
+  float* ws_o;     // [W][2][rows][max(D, 16)]  unnormalised O of partial pieces (lane-major)
 };
 
 constexpr int kWavesPerGroup = 4;
@@ -438,15 +438,16 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
     // stored -- and every other from the workspace, so the result does not
     // depend on which wave merges.
     const __amdgpu_buffer_rsrc_t ro = ws_rsrc(a.ws_o), rml = ws_rsrc(a.ws_ml);
-    // A piece's O is stored lane-major: chunk c of n-tile nt of slot sl holds
-    // the 16 bytes of each lane of a row below a.rows, lane (n, g) at g rt + n
-    // (rt rows in the tile), so each store (and load) instruction moves
-    // 64 rt consecutive bytes.  Row-major pieces made each instruction 48
-    // partial-line writes through to the coherence point, several
-    // microseconds per published piece under the K/V stream.
+    // A piece's O is stored lane-major: a slot holds a.rows * 4J 16-byte
+    // chunks; n-tile nt (rt rows) starts at chunk 64 J nt, and its chunk c
+    // holds the 16 bytes of each lane (n, g) with n < rt at g rt + n, so each
+    // store (and load) instruction moves 64 rt consecutive bytes.  Row-major
+    // pieces made each instruction 48 partial-line writes through to the
+    // coherence point, several microseconds per published piece under the
+    // K/V stream.  o_chunk is chunk 0's offset; chunk c is 64 rt c further.
+    auto o_rt = [&](int nt) { return min(16, a.rows - 16 * nt); };
     auto o_chunk = [&](long sl, int nt) -> uint32_t {
-      const int rt = min(16, a.rows - 16 * nt);
-      return (uint32_t)(((sl * NT + nt) * J * 64 + g * rt + n) * 16);
+      return (uint32_t)(((sl * a.rows + 16 * nt) * 4 * J + g * o_rt(nt) + n) * 16);
     };
     auto merge_pieces = [&](const UnitPos& uu, int wa_, int wb_, long slot_a_) {
 #pragma unroll
@@ -482,7 +483,8 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
             const uint32_t ob = o_chunk(sl, nt);
 #pragma unroll
             for (int c = 0; c < J; ++c)
-              ov[k][c] = __builtin_amdgcn_raw_buffer_load_b128(ro, ld ? ob + 1024 * c : kPastRecords, 0, kCoherent);
+              ov[k][c] = __builtin_amdgcn_raw_buffer_load_b128(ro, ld ? ob + 64 * o_rt(nt) * c : kPastRecords, 0,
+                                                               kCoherent);
           }
 #pragma unroll
           for (int k = 0; k < kMergeBatch; ++k) {
@@ -563,7 +565,7 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
             __builtin_amdgcn_raw_buffer_store_b128(
                 (u32x4){__builtin_bit_cast(uint32_t, tmp[4 * c]), __builtin_bit_cast(uint32_t, tmp[4 * c + 1]),
                         __builtin_bit_cast(uint32_t, tmp[4 * c + 2]), __builtin_bit_cast(uint32_t, tmp[4 * c + 3])},
-                ro, ob + 1024 * c, 0, kCoherent);
+                ro, ob + 64 * o_rt(nt) * c, 0, kCoherent);
           if (g == 0)
             __builtin_amdgcn_raw_buffer_store_b64(
                 (u32x2){__builtin_bit_cast(uint32_t, core.m[nt]), __builtin_bit_cast(uint32_t, lrow[nt])}, rml,

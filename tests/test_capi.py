@@ -63,12 +63,11 @@ def test_noalloc_scratch_size_matches_header():
 def _ws(waves, rows, D, units):
     # a fixed 1 MiB region of int32 arrival counters (2^18 sequence x KV-head
     # units), then per wave two partial slots of rows x (m, l) floats and two
-    # of O over whole 16-row tiles of max(D, 16) floats
+    # of rows x max(D, 16) floats of O
     if waves <= 1:
         return 0
     assert units <= 1 << 18
-    tile_rows = 16 if rows <= 16 else 32 if rows <= 32 else 64
-    return (1 << 20) + waves * (2 * rows * 2 * 4 + 2 * tile_rows * max(D, 16) * 4)
+    return (1 << 20) + waves * (2 * rows * 2 * 4 + 2 * rows * max(D, 16) * 4)
 
 
 def _waves(seqs, kv_heads, max_ctx, part_tokens):
