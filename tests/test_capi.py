@@ -88,6 +88,8 @@ def test_workspace_size(lib):
     assert _waves(256, 8, 32768, 0) == 4096
     assert lib.hpa_decode_workspace_size(256, 3, 32, 8, 128, 32768, 0) == _ws(4096, 12, 128, 2048)
     assert lib.hpa_decode_workspace_size(64, 1, 14, 2, 64, 4096, 32) == _ws(4096, 7, 64, 128)
+    # config 5 at the wave cap fits the no-alloc entry's static scratch
+    assert lib.hpa_decode_workspace_size(256, 3, 32, 8, 128, 32768, 0) <= _lib.HPA_NOALLOC_SCRATCH_BYTES
 
 
 def test_argument_errors_return_status_without_a_gpu(lib):
