@@ -135,7 +135,7 @@ static int paged_decode(const void* q, void* out, int q_dtype, const void* k_poo
   const int nt = decode_nt(rows);
   if (nt != 1) {
     // More than 16 query rows per KV head (a wide speculative verify).  With
-    // fp16 queries over an int8 pool, 17-64 rows run on the verify kernel
+    // fp16 or bf16 queries over an int8 pool, 17-64 rows run on the verify kernel
     // that dequantises in registers (the decode kernel's two and four row
     // tiles spill registers).  Otherwise, above 32 rows: the decode kernel's
     // four row tiles spill and it takes at most 64 rows, while the prefill

@@ -100,7 +100,7 @@ bool launch_prefill_mfma(const PrefillArgs& a, int q_dtype, int kv_dtype, int sc
                          int max_q_len, hipStream_t s);
 
 // A verify (uniform_q > 0) of 17-64 rows per KV head over an int8 pool
-// (fp16 queries, fp16 / fp32 scales, head_dim 64 / 128, block_size >= 16),
+// (fp16 or bf16 queries, fp16 / fp32 scales, head_dim 64 / 128, block_size >= 16),
 // dequantised in registers (hpa_verify_i8.hip); returns false (launching
 // nothing) for other shapes.
 bool launch_verify_i8(const PrefillArgs& a, int q_dtype, int kv_dtype, int scale_dtype, int head_dim, hipStream_t s);

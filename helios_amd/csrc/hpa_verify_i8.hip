@@ -1,6 +1,7 @@
 // Wide speculative verify over int8 pools: 17-64 query rows per KV head
 // (helios' verify prefill, exec/runner.py:354-362, batched over sequences),
-// fp16 queries, head_dim 64 or 128, block_size >= 16.
+// fp16 or bf16 queries (bf16 rows enter the fp16 MFMAs scaled by a power of
+// two), head_dim 64 or 128, block_size >= 16.
 //
 // A workgroup of two waves owns one (sequence, KV head): wave w holds rows
 // [32 w, 32 w + 32) of its G * q_per_seq rows, one 32x32 MFMA tile, and
