@@ -548,3 +548,52 @@ def test_metadata_tensors_are_validated():
                                    out=torch.empty(8, 2, 64, dtype=torch.float16, device="cuda").transpose(0, 1))
     with pytest.raises(ValueError, match="sum to"):
         paged_attention_varlen(q, cache, tt, torch.tensor([1, 2], dtype=torch.int32), lt - 1, lt)
+
+
+_F16, _B16, _F32 = torch.float16, torch.bfloat16, torch.float32
+# (query dtype, int8 pool, scale dtype, head_dim, Hkv, G, tokens, part_tokens):
+# every route of hpa_paged_decode at least once
+_ROUTES = [
+    (_F16, True, _F16, 128, 4, 4, 2, 0),      # int8 decode kernel, 8 rows
+    (_B16, True, _F32, 64, 2, 4, 4, 64),      # bf16 over int8, 16 rows
+    (_F16, True, _F16, 128, 2, 4, 5, 64),     # int8 verify kernel, 20 rows
+    (_B16, True, _F32, 128, 1, 7, 4, 0),      # int8 verify kernel (bf16), 28 rows
+    (_F16, True, _F32, 64, 2, 8, 6, 128),     # int8 verify kernel, 48 rows
+    (_B16, True, _F16, 128, 4, 4, 16, 64),    # int8 verify kernel (bf16), 64 rows
+    (_F16, True, _F16, 128, 2, 7, 12, 0),     # int8, 84 rows: MFMA prefill verify
+    (_B16, True, _F16, 256, 2, 4, 5, 64),     # int8 head_dim 256, two tiles
+    (_F16, False, None, 128, 4, 4, 3, 64),    # fp16 decode kernel, 12 rows
+    (_B16, False, None, 128, 2, 7, 4, 0),     # bf16 pool, 28 rows: MFMA prefill
+    (_F16, False, None, 64, 1, 8, 8, 128),    # 64 rows: MFMA prefill
+    (_F16, False, None, 128, 2, 8, 20, 64),   # 160 rows: MFMA prefill, two tiles
+    (_F16, False, None, 256, 2, 2, 12, 64),   # head_dim 256, 24 rows: decode kernel
+    (_B16, False, None, 256, 1, 7, 1, 0),     # head_dim 256 decode
+]
+
+
+@pytest.mark.parametrize("case", range(len(_ROUTES)))
+def test_every_route_on_random_contexts(case):
+    """Every route of hpa_paged_decode -- the decode kernel's one-, two- and
+    four-tile forms, the int8 verify kernel, the MFMA prefill kernel's
+    verify mode -- on seeded random contexts up to 2 500 keys, cut into
+    pieces by a small part_tokens where given.  Int8 verifies above 64 rows
+    run over the dequantised values rounded to the compute dtype (helios'
+    gather), so they are held to that oracle; everything else to the exact
+    one."""
+    dtype, quant, scale_dtype, D, Hkv, G, T, part = _ROUTES[case]
+    rng = np.random.default_rng(1000 + case)
+    n = int(rng.integers(2, 7))
+    lens = sorted(int(x) for x in rng.integers(T, 2500, size=n))
+    rows = G * T
+    print(f"case {case}: {dtype} int8 {quant} ({scale_dtype}) D {D} Hkv {Hkv} G {G} T {T} rows {rows} "
+          f"lens {lens} part {part}", flush=True)
+    cache, tables, q = _case(2000 + case, n, lens, G * Hkv, Hkv, D, 16, dtype, quant=quant,
+                             scale_dtype=scale_dtype or torch.float16, q_per_seq=T)
+    ks, vs = cache._scales()
+    got = paged_attention_decode_hip(q, cache.k_cache, cache.v_cache, tables, lens, 1 / math.sqrt(D), ks, vs,
+                                     q_per_seq=T, part_tokens=part)
+    pool = pool_dequantized(cache) if quant and rows > 64 else pool_of(cache)
+    qn = to_np(q).astype(np.float32)
+    want = (R.paged_decode_batched(qn, pool, tables, lens, 1 / math.sqrt(D)) if T == 1 else
+            R.paged_verify_batched(qn, pool, tables, lens, T, 1 / math.sqrt(D)))
+    _check(got, want, dtype, f"route case {case}")
