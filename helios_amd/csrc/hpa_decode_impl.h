@@ -64,11 +64,14 @@ constexpr int kWaveCap = 4096;          // 256 CUs x 16 resident waves
 // younger one finishes long after the older, while a single wave with a deep
 // pipeline keeps the SIMD's share of HBM busy on its own.
 constexpr int kDepth = 3;
-// head_dim 256 keeps one step in flight: a step's K/V registers (64 VGPRs per
-// tensor for 16-bit pools) times a ring of four spilled over a thousand
-// registers to scratch, which cost two thirds of the bandwidth
-template <int D>
-constexpr int ring_depth() { return D >= 256 ? 1 : kDepth; }
+// head_dim 256, and key rows of 512 bytes or more (fp32 pools at head_dim
+// 128), keep one step in flight: a step's K/V registers (64 VGPRs per tensor)
+// times a ring of four spilled over a thousand registers to scratch, which
+// cost two thirds of the bandwidth
+template <int D, class KVT>
+constexpr int ring_depth() {
+  return D >= 256 || D * (int)sizeof(typename KVT::storage) >= 512 ? 1 : kDepth;
+}
 constexpr int kDefaultMinTokens = 256;  // per-wave slice floor (8 steps)
 // What a unit costs beyond its steps, in step-equivalents: its prologue
 // (table window, query rows, first loads in flight) and epilogue (output or
@@ -259,7 +262,7 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
   u.kvh = head;
 
   const typename Core::LaneOff lo = Core::lane_off();
-  constexpr int DEP = ring_depth<D>();
+  constexpr int DEP = ring_depth<D, KVT>();
   constexpr int NB = DEP + 1;
   // A ring of DEP + 1 register buffers, unrolled so every index is a
   // compile-time constant: DEP steps of loads stay in flight while a step
