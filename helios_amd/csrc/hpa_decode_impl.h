@@ -68,9 +68,10 @@ constexpr int kDepth = 3;
 // 128), keep one step in flight: a step's K/V registers (64 VGPRs per tensor)
 // times a ring of four spilled over a thousand registers to scratch, which
 // cost two thirds of the bandwidth
-template <int D, class KVT>
+template <int D, class KVT, int NT>
 constexpr int ring_depth() {
-  return D >= 256 || D * (int)sizeof(typename KVT::storage) >= 512 ? 1 : kDepth;
+  constexpr int rowb = D * (int)sizeof(typename KVT::storage);
+  return D >= 256 || rowb >= 512 ? 1 : NT >= 4 && rowb >= 128 ? 1 : NT >= 2 && rowb >= 256 ? 2 : kDepth;
 }
 constexpr int kDefaultMinTokens = 256;  // per-wave slice floor (8 steps)
 // What a unit costs beyond its steps, in step-equivalents: its prologue
@@ -262,7 +263,7 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void decode_kernel(const Decod
   u.kvh = head;
 
   const typename Core::LaneOff lo = Core::lane_off();
-  constexpr int DEP = ring_depth<D, KVT>();
+  constexpr int DEP = ring_depth<D, KVT, NT>();
   constexpr int NB = DEP + 1;
   // A ring of DEP + 1 register buffers, unrolled so every index is a
   // compile-time constant: DEP steps of loads stay in flight while a step
