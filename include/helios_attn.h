@@ -86,11 +86,12 @@ size_t hpa_decode_workspace_size(int num_seqs, int q_per_seq, int num_q_heads, i
  * pool (head_dim 64 or 128, block_size >= 16) run on a verify kernel that
  * dequantises in registers; it uses the workspace, when given, to cut long
  * contexts (fewer cuts with a smaller one).  Over fp16 / bf16 pools, 17 rows
- * and more, and other shapes above 32 rows, run on the prefill kernels (the
- * MFMA one when it takes the shape: fp16 / bf16 queries, head_dim 64 or
- * 128, block_size >= 16; else above 32 rows the generic one), with the same
- * results as hpa_paged_prefill over the same tokens; the workspace is then
- * unused.
+ * and more, and other shapes above 32 rows, run on the MFMA prefill kernel
+ * when it takes the shape (fp16 / bf16 queries, head_dim 64 or 128,
+ * block_size >= 16), and above 64 rows on the generic prefill kernel when it
+ * does not, with the same results as hpa_paged_prefill over the same tokens;
+ * the workspace is then unused.  Up to 64 rows the shapes no other kernel
+ * takes run on the decode kernel.
  * part_tokens: smallest share of the context, in tokens, one wave streams
  * (0 = library default); it changes only the summation order.
  * workspace: at least hpa_decode_workspace_size(...) bytes of device memory
