@@ -135,20 +135,17 @@ static int paged_decode(const void* q, void* out, int q_dtype, const void* k_poo
   const int nt = decode_nt(rows);
   if (nt != 1) {
     // More than 16 query rows per KV head (a wide speculative verify).  With
-    // fp16 or bf16 queries over an int8 pool, 17-64 rows run on the verify kernel
-    // that dequantises in registers (the decode kernel's two and four row
-    // tiles spill registers).  Otherwise, above 32 rows: the decode kernel's
-    // four row tiles spill and it takes at most 64 rows, while the prefill
-    // kernels tile any number of rows.  The MFMA prefill kernel (fp16 / bf16
-    // queries, head_dim 64 / 128, block_size >= 16) runs these verifies
-    // several times faster; past 64 rows, shapes it does not take run on the
-    // generic prefill kernel.  Both compute the same causal rule as
-    // hpa_paged_prefill over the same tokens, in a mode where sequence b's
-    // tokens are [b q_per_seq, (b + 1) q_per_seq) and end at its context; no
-    // workspace is used.  17-32 rows over fp16 / bf16 pools take the MFMA
-    // prefill kernel too (the decode kernel's two row tiles spill: 980 us
-    // against 470 us at config 5's batch); over int8 pools the verify kernel
-    // or else the decode kernel runs them.
+    // fp16 or bf16 queries over an int8 pool, 17-64 rows run on the verify
+    // kernel that dequantises in registers.  Over fp16 / bf16 pools, and for
+    // other shapes above 32 rows, the MFMA prefill kernel (fp16 / bf16
+    // queries, head_dim 64 / 128, block_size >= 16) runs the verify, about
+    // twice as fast as the decode kernel's two and four row tiles; past 64
+    // rows, which the decode kernel does not take, shapes the MFMA kernel does
+    // not take run on the generic prefill kernel.  Both prefill kernels
+    // compute the same causal rule as hpa_paged_prefill over the same tokens,
+    // in a mode where sequence b's tokens are [b q_per_seq, (b + 1) q_per_seq)
+    // and end at its context; no workspace is used.  Up to 64 rows, shapes no
+    // other kernel takes run on the decode kernel.
     PrefillArgs pa;
     pa.q = q;
     pa.out = out;
