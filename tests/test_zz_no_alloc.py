@@ -78,3 +78,27 @@ def test_noalloc_refuses_shapes_beyond_its_scratch():
                                       16, 1, 256, 16, 1, 32768, ctypes.c_float(0.0625), 0, stream_ptr(dev))
     assert st == _lib.HPA_ERR_WORKSPACE
     assert b"static scratch" in lib.hpa_last_error()
+
+
+def test_noalloc_at_config5_full_size():
+    """Config 5's own batch (256 sequences x 3 tokens, Llama-8B int8 pool, the
+    wave cap's workspace, ~50 MiB of the 64 MiB scratch): the no-alloc entry
+    point equals hpa_paged_decode with a caller workspace bit for bit, twice
+    in a row (the scratch keeps the counters at zero between calls)."""
+    import bench
+
+    lib = _lib.lib()
+    dev = torch.device("cuda:0")
+    print("noalloc decode at config 5's full size", flush=True)
+    wl = bench.DecodeWorkload(5, dev, 4)
+    cache = wl.caches[0]
+    need = lib.hpa_decode_workspace_size(wl.B, wl.Tq, wl.Hq, wl.Hkv, wl.D, wl.max_ctx, 0)
+    assert 0 < need <= _lib.HPA_NOALLOC_SCRATCH_BYTES
+    want = wl.step().clone()
+    for _ in range(2):
+        got = torch.full_like(wl.q, float("nan"))
+        st = lib.hpa_paged_decode_noalloc(*_args(wl.q, got, cache, wl.tables_t, wl.lens_t, wl.Tq, wl.max_ctx, 0),
+                                          stream_ptr(dev))
+        _lib.check(st, "hpa_paged_decode_noalloc")
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), "noalloc differs from the workspace entry point at config 5"
