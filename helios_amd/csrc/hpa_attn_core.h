@@ -165,8 +165,8 @@ struct AttnCore {
   //
   // Over int8 pools the MFMAs run in fp16 for bf16 queries too (MT, the math
   // type): a bf16 value is exact in fp16 within fp16's range, and each
-  // query row enters scaled by a power of two that brings its largest
-  // element below 2^15 (the scale returns in the row's score scale), so
+  // query row enters scaled by the power of two that brings its largest
+  // element into [2^14, 2^15) (the scale returns in the row's score scale), so
   // the cheap fp16 form of the dequantisation serves both.  The output is
   // still written in the query dtype.
   typedef typename std::conditional<QUANT && std::is_same<CT, BF16>::value, F16, CT>::type MT;
@@ -185,7 +185,7 @@ struct AttnCore {
   f32x4 o[NT][J];
   f32x4 ps[NT];     // I8F16: sum over keys of the fp16 P' fed to the PV MFMAs
   float qoff[NT];   // I8F16: 128 * 2^-24 * sum_d q[row][d]
-  float qexp[NT];   // bf16 queries over int8: the power of two the row was scaled down by
+  float qexp[NT];   // bf16 queries over int8: 2^e, the row entered fp16 as row * 2^-e
   float m[NT], l[NT];
   int lim[NT];
 

@@ -64,14 +64,20 @@ constexpr int kWaveCap = 4096;          // 256 CUs x 16 resident waves
 // younger one finishes long after the older, while a single wave with a deep
 // pipeline keeps the SIMD's share of HBM busy on its own.
 constexpr int kDepth = 3;
-// head_dim 256, and key rows of 512 bytes or more (fp32 pools at head_dim
-// 128), keep one step in flight: a step's K/V registers (64 VGPRs per tensor)
-// times a ring of four spilled over a thousand registers to scratch, which
-// cost two thirds of the bandwidth
+// Steps of loads in flight, where kDepth's ring would spill: head_dim 256,
+// and key rows of 512 bytes or more (fp32 pools at head_dim 128), keep one (a
+// step's K/V registers, 64 VGPRs per tensor, times a ring of four spilled
+// over a thousand registers to scratch and cost two thirds of the
+// bandwidth); with more row tiles, 256-byte rows keep two at two tiles and
+// one at four, and int8 rows of head_dim 128 one at four tiles.
 template <int D, class KVT, int NT>
 constexpr int ring_depth() {
   constexpr int rowb = D * (int)sizeof(typename KVT::storage);
-  return D >= 256 || rowb >= 512 ? 1 : NT >= 4 && rowb >= 128 ? 1 : NT >= 2 && rowb >= 256 ? 2 : kDepth;
+  constexpr bool i8 = sizeof(typename KVT::storage) == 1;
+  if (D >= 256 || rowb >= 512) return 1;
+  if (NT >= 4 && (rowb >= 256 || (i8 && D >= 128))) return 1;
+  if (NT >= 2 && rowb >= 256) return 2;
+  return kDepth;
 }
 constexpr int kDefaultMinTokens = 256;  // per-wave slice floor (8 steps)
 // What a unit costs beyond its steps, in step-equivalents: its prologue

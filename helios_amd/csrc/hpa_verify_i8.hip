@@ -284,7 +284,7 @@ __global__ __launch_bounds__(64 * kViWaves, 2) void verify_i8_kernel(const Prefi
   float qs = 0.f;
 #pragma unroll
   for (int c = 0; c < CH; ++c) qf[c] = rv ? *reinterpret_cast<const u32x4*>(qrow + 16 * c + 8 * h) : (u32x4){0, 0, 0, 0};
-  float qexp = 1.f;  // bf16: the power of two the row was scaled down by
+  float qexp = 1.f;  // bf16: 2^e, the row entered fp16 as row * 2^-e
   if constexpr (BQ) {
     float mx = 0.f;
 #pragma unroll
