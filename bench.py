@@ -80,8 +80,9 @@ def _fill_by_writes(cache, lens, tables_t, gen, device, chunk_tokens=1 << 19):
         while j < len(lens) and (tok == 0 or tok + lens[j] <= chunk_tokens):
             tok += lens[j]
             j += 1
-        k = torch.randn(tok, H, D, generator=gen, device=device, dtype=torch.float16)
-        v = torch.randn(tok, H, D, generator=gen, device=device, dtype=torch.float16)
+        vdt = torch.bfloat16 if cache.dtype == torch.bfloat16 else torch.float16
+        k = torch.randn(tok, H, D, generator=gen, device=device, dtype=vdt)
+        v = torch.randn(tok, H, D, generator=gen, device=device, dtype=vdt)
         write_kv(cache, tables_t[i:j], [0] * (j - i), k, v, query_lens=lens[i:j])
         i = j
     torch.cuda.synchronize()
@@ -90,7 +91,7 @@ def _fill_by_writes(cache, lens, tables_t, gen, device, chunk_tokens=1 << 19):
 class DecodeWorkload(Workload):
     """Configs 2, 3 and 5: batched decode (q_per_seq 1) or verify (3)."""
 
-    def __init__(self, cfg, device, seed, part_tokens=0, copies=1, scale_dtype=None):
+    def __init__(self, cfg, device, seed, part_tokens=0, copies=1, scale_dtype=None, qdtype=None):
         import numpy as np
         import torch
 
@@ -113,7 +114,9 @@ class DecodeWorkload(Workload):
             self.name = "toy-fp32-decode (config 1)"
             B, Hq, Hkv, D, Tq, quant = 4, 4, 2, 64, 1, False
             lens = [int(x) for x in rng.integers(17, 101, size=B)]
-        dtype = torch.float32 if cfg == 1 else torch.float16
+        dtype = torch.float32 if cfg == 1 else (qdtype or torch.float16)
+        if dtype == torch.bfloat16:
+            self.name += ", bf16 queries"
         self.B, self.Hq, self.Hkv, self.D, self.Tq, self.quant = B, Hq, Hkv, D, Tq, quant
         self.lens = lens
         nb, self.tables_t, self.tables_np = _shuffled_tables(rng, lens, device)
@@ -175,8 +178,9 @@ class DecodeWorkload(Workload):
 
         return {"workload": self.name, "batch": self.B, "q_per_seq": self.Tq,
                 "n_q_heads": self.Hq, "n_kv_heads": self.Hkv, "head_dim": self.D,
-                "block_size": BLOCK, "kv_dtype": "int8" if self.quant else
-                ("fp32" if self.cfg == 1 else "fp16"),
+                "block_size": BLOCK, "q_dtype": str(self.q.dtype).replace("torch.", ""),
+                "kv_dtype": "int8" if self.quant else
+                ("fp32" if self.cfg == 1 else ("bf16" if self.q.dtype == torch.bfloat16 else "fp16")),
                 "scale_dtype": ("fp32" if self.scale_dtype == torch.float32 else "fp16") if self.quant else None,
                 "context": {"mean": round(sum(self.lens) / len(self.lens), 1),
                             "max": self.max_ctx, "min": min(self.lens)},
@@ -192,14 +196,14 @@ class DecodeWorkload(Workload):
 
         c = self.caches[0]
         pool = R.PagedPool(c.num_blocks, BLOCK, self.Hkv, self.D, np.float32, quantized=self.quant)
-        pool.k = c.k_cache.cpu().numpy()
-        pool.v = c.v_cache.cpu().numpy()
         if self.quant:
+            pool.k = c.k_cache.cpu().numpy()
+            pool.v = c.v_cache.cpu().numpy()
             pool.k_scale = c.k_scale.cpu().numpy()
             pool.v_scale = c.v_scale.cpu().numpy()
-        else:
-            pool.k = pool.k.astype(np.float32)
-            pool.v = pool.v.astype(np.float32)
+        else:  # (numpy has no bf16: through fp32, which holds every value)
+            pool.k = c.k_cache.float().cpu().numpy()
+            pool.v = c.v_cache.float().cpu().numpy()
         q = self.q.float().cpu().numpy()
         tabs = [list(self.tables_np[i, :(n + BLOCK - 1) // BLOCK]) for i, n in enumerate(self.lens)]
         done, t0 = 0, time.perf_counter()
@@ -562,7 +566,7 @@ def graph_bench(device, cfg, layers, steps, warmup):
     }))
 
 
-def spec_bench(device, gamma, steps, warmup, seed=4):
+def spec_bench(device, gamma, steps, warmup, seed=4, qdtype=None):
     """Attention work of one speculative step for config 5's batch, one
     layer: gamma draft decodes over an int8 KV shadow (each writing its
     token), the verify pass (gamma tokens per sequence written to and
@@ -576,9 +580,10 @@ def spec_bench(device, gamma, steps, warmup, seed=4):
 
     import helios_amd as H
 
-    wl = DecodeWorkload(5, device, seed)
+    wl = DecodeWorkload(5, device, seed, qdtype=qdtype)
+    dt = wl.q.dtype
     target = wl.caches[0]
-    shadow = H.QuantizedPagedKVCache(target.num_blocks, BLOCK, wl.Hkv, wl.D, dtype=torch.float16,
+    shadow = H.QuantizedPagedKVCache(target.num_blocks, BLOCK, wl.Hkv, wl.D, dtype=dt,
                                      device=device, scale_dtype=torch.float16)
     for a, b in ((shadow.k_cache, target.k_cache), (shadow.v_cache, target.v_cache),
                  (shadow.k_scale, target.k_scale), (shadow.v_scale, target.v_scale)):
@@ -589,10 +594,10 @@ def spec_bench(device, gamma, steps, warmup, seed=4):
     tables = [[int(x) for x in row[: (c + BLOCK - 1) // BLOCK]] for row, c in zip(wl.tables_np, wl.lens)]
     tabs = H.DeviceBlockTables.for_cache(target, B, max(len(t) for t in tables))
     gen = torch.Generator(device=device).manual_seed(seed)
-    q1 = torch.randn(B, Hq, D, generator=gen, device=device, dtype=torch.float16)
-    k1 = torch.randn(B, Hkv, D, generator=gen, device=device, dtype=torch.float16)
-    qg = torch.randn(B * gamma, Hq, D, generator=gen, device=device, dtype=torch.float16)
-    kg = torch.randn(B * gamma, Hkv, D, generator=gen, device=device, dtype=torch.float16)
+    q1 = torch.randn(B, Hq, D, generator=gen, device=device, dtype=dt)
+    k1 = torch.randn(B, Hkv, D, generator=gen, device=device, dtype=dt)
+    qg = torch.randn(B * gamma, Hq, D, generator=gen, device=device, dtype=dt)
+    kg = torch.randn(B * gamma, Hkv, D, generator=gen, device=device, dtype=dt)
     base = tabs.prepare(range(B), tables, lens, [c - 1 for c in lens], [1] * B, True)
     drafts = [base.advanced(j) for j in range(gamma)]
     vm = base.verify(gamma)
@@ -643,7 +648,7 @@ def spec_bench(device, gamma, steps, warmup, seed=4):
         "launches_batched": 2 * (gamma + 2), "launches_per_sequence": 2 * (gamma + 2) * B,
         "hbm_gbs_batched": round(alg / (res["batched"] * 1e-3) / 1e9, 1),
         "algorithmic_bytes": int(alg),
-        "config": {"workload": wl.name, "batch": B, "gamma": gamma},
+        "config": {"workload": wl.name, "batch": B, "gamma": gamma, "q_dtype": str(dt).replace("torch.", "")},
     }))
 
 
@@ -735,6 +740,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", type=int, default=5, choices=[1, 2, 3, 4, 5])
     ap.add_argument("--seed", type=int, default=None)
+    ap.add_argument("--dtype", choices=["fp16", "bf16"], default="fp16",
+                    help="query (and fp pool) dtype of the decode configs 2, 3, 5 and --spec-gamma")
     ap.add_argument("--kv-int8", action="store_true",
                     help="config 4 on an int8 pool (the same values quantized by the write kernel)")
     ap.add_argument("--part-tokens", type=int, default=0,
@@ -786,6 +793,7 @@ def main():
 
     import helios_amd  # noqa: F401
 
+    qdt = torch.bfloat16 if args.dtype == "bf16" else torch.float16
     if not torch.cuda.is_available():
         raise SystemExit("bench.py needs a GPU")
     device = torch.device("cuda:0")
@@ -793,7 +801,7 @@ def main():
         graph_bench(device, args.config, args.graph_layers, min(args.steps, 100), min(args.warmup, 20))
         return
     if args.spec_gamma:
-        spec_bench(device, args.spec_gamma, min(args.steps, 50), min(args.warmup, 20))
+        spec_bench(device, args.spec_gamma, min(args.steps, 50), min(args.warmup, 20), qdtype=qdt)
         return
     if args.helios_shape:
         helios_shape_bench(device, args.steps, args.warmup)
@@ -809,7 +817,8 @@ def main():
         copies = args.copies
         if copies is None:
             copies = 1 if args.config in (1, 5) else 5
-        wl = DecodeWorkload(args.config, device, seed, args.part_tokens, copies)
+        wl = DecodeWorkload(args.config, device, seed, args.part_tokens, copies,
+                            qdtype=qdt if args.config in (2, 3, 5) else None)
 
     print(f"bench: {wl.name} built; timing {args.steps} steps", file=sys.stderr, flush=True)
     ms_step, ms_run, warm_done, wall = time_steps(wl, args.steps, args.warmup, args.warmup_s)
@@ -835,8 +844,9 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8-kv/fp16" if (getattr(wl, "quant", False) or getattr(wl, "kv_int8", False)) else
-        ("f32" if args.config == 1 else "f16"),
+        "dtype": ("int8-kv/" + ("bf16" if qdt == torch.bfloat16 and args.config != 4 else "fp16"))
+        if (getattr(wl, "quant", False) or getattr(wl, "kv_int8", False)) else
+        ("f32" if args.config == 1 else ("bf16" if qdt == torch.bfloat16 and args.config != 4 else "f16")),
         "data": "synthetic (seeded N(0,1); int8 KV quantized on the GPU by the library's write kernel)",
         "config": wl.config(),
         "roofline": roofline(wl, ms_step, key),
