@@ -560,6 +560,7 @@ _ROUTES = [
     (_B16, True, _F32, 128, 1, 7, 4, 0),      # int8 verify kernel (bf16), 28 rows
     (_F16, True, _F32, 64, 2, 8, 6, 128),     # int8 verify kernel, 48 rows
     (_B16, True, _F16, 128, 4, 4, 16, 64),    # int8 verify kernel (bf16), 64 rows
+    (_B16, True, _F32, 64, 2, 4, 6, 64),      # int8 verify kernel (bf16), head_dim 64, 24 rows
     (_F16, True, _F16, 128, 2, 7, 12, 0),     # int8, 84 rows: MFMA prefill verify
     (_B16, True, _F16, 256, 2, 4, 5, 64),     # int8 head_dim 256, two tiles
     (_F16, False, None, 128, 4, 4, 3, 64),    # fp16 decode kernel, 12 rows
