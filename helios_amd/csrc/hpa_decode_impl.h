@@ -69,14 +69,15 @@ constexpr int kDepth = 3;
 // step's K/V registers, 64 VGPRs per tensor, times a ring of four spilled
 // over a thousand registers to scratch and cost two thirds of the
 // bandwidth); with more row tiles, 256-byte rows keep two at two tiles and
-// one at four, and int8 rows of head_dim 128 one at four tiles.
+// one at four, and int8 rows of head_dim 128 two at two tiles and one at
+// four.
 template <int D, class KVT, int NT>
 constexpr int ring_depth() {
   constexpr int rowb = D * (int)sizeof(typename KVT::storage);
   constexpr bool i8 = sizeof(typename KVT::storage) == 1;
   if (D >= 256 || rowb >= 512) return 1;
   if (NT >= 4 && (rowb >= 256 || (i8 && D >= 128))) return 1;
-  if (NT >= 2 && rowb >= 256) return 2;
+  if (NT >= 2 && (rowb >= 256 || (i8 && D >= 128))) return 2;
   return kDepth;
 }
 constexpr int kDefaultMinTokens = 256;  // per-wave slice floor (8 steps)
