@@ -208,8 +208,12 @@ __global__ __launch_bounds__(256) void kv_gather_kernel(const GatherArgs a) {
       typedef typename ST::storage s_t;
       const float sk = Cvt<ST>::to_f32(reinterpret_cast<const s_t*>(a.ks)[slot]);
       const float sv = Cvt<ST>::to_f32(reinterpret_cast<const s_t*>(a.vs)[slot]);
+      // helios rounds the product to fp32, then to the output dtype: the
+      // empty asm keeps the compiler from fusing the two roundings into one
+      // mixed-precision multiply (with fp32 scales the product is not exact)
       kx = (float)reinterpret_cast<const int8_t*>(a.kp)[slot * D + d] * sk;
       vx = (float)reinterpret_cast<const int8_t*>(a.vp)[slot * D + d] * sv;
+      asm volatile("" : "+v"(kx), "+v"(vx));
     } else {
       typedef typename PT::storage p_t;
       kx = Cvt<PT>::to_f32(reinterpret_cast<const p_t*>(a.kp)[slot * D + d]);

@@ -109,7 +109,10 @@ __device__ __forceinline__ void dequant_words(const uint32_t* in, uint32_t sbits
     }
   } else {
     // fp32: byte q ^ 0x80 = q + 128 exactly; fma(q + 128, s, -128 s) is
-    // q * s rounded once (-128 s is exact), then rounded to CT
+    // q * s rounded once to fp32 (-128 s is exact), then rounded to CT.  The
+    // empty asm keeps the compiler from fusing the two roundings into one
+    // mixed-precision fma: with fp32 scales the product is not exact, and
+    // the reference rounds it to fp32 first.
     const float s = std::is_same<ST, F16>::value ? f16_bits_to_f32(sbits & 0xffffu) : __builtin_bit_cast(float, sbits);
     const float c = -128.f * s;
 #pragma unroll
@@ -118,6 +121,7 @@ __device__ __forceinline__ void dequant_words(const uint32_t* in, uint32_t sbits
       float f[4];
 #pragma unroll
       for (int k = 0; k < 4; ++k) f[k] = __builtin_fmaf((float)((x >> (8 * k)) & 0xffu), s, c);
+      asm volatile("" : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]));
       out[2 * w] = M32<CT>::pack(f[0], f[1]);
       out[2 * w + 1] = M32<CT>::pack(f[2], f[3]);
     }

@@ -110,16 +110,26 @@ def test_fp_write_and_gather_round_trip(dtype):
     assert torch.equal(gk[4:7], k32.to(dtype))
 
 
-def test_int8_gather_dequantises_like_helios():
+@pytest.mark.parametrize("scale_dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_int8_gather_dequantises_like_helios(scale_dtype, dtype):
+    """(q.float() * s.float()).to(dtype), bit for bit: with fp32 scales the
+    product is rounded to fp32 and then to the compute dtype, two roundings
+    that must not be fused into one (300 sequences' worth of products, so
+    the rare double-rounding cases occur)."""
     gen = torch.Generator().manual_seed(0)
-    cache = QuantizedPagedKVCache(8, 16, 2, 64, dtype=torch.float16, device="cuda")
-    pool = R.PagedPool(8, 16, 2, 64, np.float16, quantized=True)
-    k = torch.randn(30, 2, 64, generator=gen)
-    cache.write([5, 1], 0, k.cuda(), k.cuda())
-    pool.write([5, 1], 0, k.numpy(), k.numpy())
-    gk, gv = cache.gather([5, 1], 30)
-    wk, wv = pool.gather([5, 1], 30)
-    assert np.array_equal(to_np(gk), wk) and np.array_equal(to_np(gv), wv)
+    cache = QuantizedPagedKVCache(40, 16, 2, 64, dtype=dtype, device="cuda", scale_dtype=scale_dtype)
+    pool = R.PagedPool(40, 16, 2, 64, np.float16 if dtype == torch.float16 else "bfloat16", quantized=True,
+                       scale_dtype=np.float16 if scale_dtype == torch.float16 else np.float32)
+    blocks = [int(x) for x in np.random.default_rng(0).permutation(40)]
+    k = torch.randn(640, 2, 64, generator=gen) * torch.rand(640, 2, 1, generator=gen) * 7
+    v = torch.randn(640, 2, 64, generator=gen)
+    cache.write(blocks, 0, k.cuda(), v.cuda())
+    pool.write(blocks, 0, k.numpy(), v.numpy())
+    gk, gv = cache.gather(blocks, 640)
+    wk, wv = pool.gather(blocks, 640)
+    assert np.array_equal(to_np(gk.float()), np.asarray(wk, np.float32))
+    assert np.array_equal(to_np(gv.float()), np.asarray(wv, np.float32))
 
 
 def test_partial_block_write_and_out_of_range():
