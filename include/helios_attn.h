@@ -113,7 +113,10 @@ int hpa_paged_decode(const void* q, void* out, int q_dtype, const void* k_pool, 
 
 /* hpa_paged_decode for callers that cannot allocate (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc): the same
- * arguments and results, with the split-K workspace taken from a static
+ * arguments and results (bit for bit, except 17-64-row int8 verifies, which
+ * it runs without cutting units: there it agrees within the fp16 bound, as
+ * hpa_paged_decode does across workspace sizes), with the split-K workspace
+ * taken from a static
  * device array of HPA_NOALLOC_SCRATCH_BYTES that the library holds on each
  * GPU it runs on until the process ends.  It calls no hipMalloc, hipFree or
  * allocating routine.  Each call first clears the arrival counters it uses
